@@ -1,0 +1,118 @@
+/*
+ * fxpr.h - C ABI of the MI355X (gfx950) fixed-point reduction kernels.
+ *
+ * Every entry point takes raw device pointers, element counts and strides,
+ * launches asynchronously on the given HIP stream (a hipStream_t passed as
+ * void*; NULL = the null stream), never allocates device memory and never
+ * synchronises. Return value: 0 on success, a negative FXPR_E_* code when the
+ * arguments are rejected before launch, or a positive hipError_t when the
+ * launch itself failed. fxpr_error_string() turns either into text.
+ *
+ * Each function replaces the device half of one reference operator of the
+ * `fxpr` torch.library namespace (fxpr_vllm/_lib.py:15-33 in
+ * Gursukh/vLLM-Triton-Fixed-Point-Reductions); the citation above each
+ * declaration names the Triton launcher and kernel it stands in for. The
+ * Python side (fxpr_vllm/_lib.py of this package) keeps the reference's
+ * schemas, validation and output allocation and calls these through ctypes.
+ */
+#ifndef FXPR_H
+#define FXPR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+enum {
+  FXPR_DTYPE_F16 = 0,
+  FXPR_DTYPE_BF16 = 1,
+  FXPR_DTYPE_F32 = 2,
+  FXPR_DTYPE_F64 = 3,
+  FXPR_DTYPE_I16 = 4,
+  FXPR_DTYPE_I32 = 5,
+  FXPR_DTYPE_I64 = 6
+};
+
+/* Negative return codes (argument errors, nothing was launched). */
+enum {
+  FXPR_OK = 0,
+  FXPR_E_DTYPE = -1,     /* element type not supported by this entry point */
+  FXPR_E_BITS = -2,      /* int_bits / frac_bits / float_bits out of range */
+  FXPR_E_SHAPE = -3,     /* negative or inconsistent sizes */
+  FXPR_E_WORKSPACE = -4, /* workspace missing or smaller than required */
+  FXPR_E_ARG = -5        /* any other invalid argument */
+};
+
+/* Text for a return code of any entry point (static storage). */
+const char* fxpr_error_string(int code);
+
+/* ABI revision of this header; bumped on any signature change. */
+int fxpr_abi_version(void);
+
+/*
+ * q[i] = RNE_sat_b(fl32(x[i]) * 2^frac_bits), NaN -> 0.
+ * x: f16 / f32 / f64 (f64 is rounded to f32 first), contiguous, n elements.
+ * q: int16 / int32 / int64 for int_bits 16 / 32 / 64. frac_bits in [0, 63].
+ * Replaces float_to_fixed_run + _float_to_fixed_kernel
+ * (fxpr_vllm/_triton/casts.py:57-89, 21-37; fxp.py:92-108).
+ */
+int fxpr_float_to_fixed(const void* x, int x_dtype, void* q, int int_bits,
+                        int frac_bits, int64_t n, void* stream);
+
+/*
+ * y[i] = OUT(fl32(q[i]) * 2^-frac_bits) with OUT = f16 / f32 / f64 for
+ * float_bits 16 / 32 / 64 (f64 widens the fp32 value).
+ * q: int16 / int32 / int64, contiguous, n elements.
+ * Replaces fixed_to_float_run + _fixed_to_float_kernel
+ * (fxpr_vllm/_triton/casts.py:92-126, 40-54; fxp.py:111-113).
+ */
+int fxpr_fixed_to_float(const void* q, int q_dtype, void* y, int float_bits,
+                        int frac_bits, int64_t n, void* stream);
+
+/*
+ * out[r] = sat_b(sum_j q[r, j]) over a contiguous [rows, cols] integer
+ * matrix: the sum is exact (64-bit for int16/int32 inputs, 128-bit for int64)
+ * and saturated once into the int_bits range; out has int_bits width.
+ * The reference has no kernel for this: it is the fixed-point sum its tests
+ * perform with torch (fxpr_vllm/_tests/test_sum.py:12-16).
+ */
+int fxpr_fixed_row_sum(const void* q, int q_dtype, void* out, int int_bits,
+                       int64_t rows, int64_t cols, void* stream);
+
+/*
+ * Deterministic RMSNorm over contiguous [rows, hidden] rows of x (f32, f16
+ * or bf16; weight and y share that type). With residual != NULL the fused
+ * form runs: v = x + residual is written back into residual (rounded to the
+ * I/O type) and normalised. The sum of squares is a fixed-point integer sum:
+ * each fl32(v*v) is cast with float_to_fixed(int_bits, frac_bits) and the
+ * row total is exact-then-saturated, so it is independent of the reduction
+ * order. rrms = 1 / sqrt(total / hidden + eps) with IEEE sqrt and division,
+ * y = IO((u * w) * rrms) where u is the (rounded) value that was stored.
+ * Replaces rms_norm_fxp_run / rms_norm_fxp_residual_run + _rms_norm_kernel
+ * (fxpr_vllm/_triton/rms_norm.py:137-151, 78-134, 19-64).
+ */
+int fxpr_rms_norm(const void* x, void* residual, const void* weight, void* y,
+                  int io_dtype, int64_t rows, int64_t hidden, float eps,
+                  int int_bits, int frac_bits, void* stream);
+
+/*
+ * Deterministic log-softmax over contiguous [rows, cols] rows of x (f32, f16
+ * or bf16) into y (same type or f32). Per row: m = max x, e_j = exp(x_j - m)
+ * by this library's fixed fp32 polynomial, S = exact-then-saturated sum of
+ * float_to_fixed(e_j, int_bits, frac_bits), lse = m + log(S * 2^-frac_bits)
+ * by the matching fixed polynomial, y_j = OUT(x_j - lse).
+ * No counterpart kernel exists in the reference: it lists
+ * fxpr_vllm/_triton/softmax.py (README.md:60) but does not ship it.
+ */
+int fxpr_log_softmax(const void* x, int x_dtype, void* y, int y_dtype,
+                     int64_t rows, int64_t cols, int int_bits, int frac_bits,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FXPR_H */

@@ -1,0 +1,266 @@
+"""GPU parity: fixed_row_sum, RMSNorm(+residual), log-softmax vs the oracle.
+
+Bit-exact against the oracle on seeded inputs (ragged, tiny, wider than the
+register cache, misaligned), the reference's own RMSNorm tolerance and
+permutation tests (fxpr_vllm/_tests/test_rms_norm.py) and sum tests
+(fxpr_vllm/_tests/test_sum.py) restated, batch invariance, and run-to-run
+identity.
+"""
+
+from __future__ import annotations
+
+import json
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+import fxpr_vllm  # noqa: F401
+from fxpr_vllm import config as fxpr_config
+from fxpr_vllm._kernels import rows as K
+from oracle import numerics as N
+from oracle import rows as R
+from tests._util import IO_NAME, from_np, mismatch_report, nan_aware_equal, seeded, to_np
+
+pytestmark = pytest.mark.gpu
+KATS = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+DEV = "cuda"
+BITS = [(32, 16), (64, 32), (16, 8), (64, 16)]
+
+
+# --------------------------------------------------------------------------
+# fixed_row_sum
+
+
+@pytest.mark.parametrize("qdtype", [torch.int16, torch.int32, torch.int64])
+@pytest.mark.parametrize("b", [16, 32, 64])
+@pytest.mark.parametrize("shape", [(7, 1000), (1, 100_003), (300, 3), (5,)])
+def test_row_sum_bit_exact(qdtype, b, shape):
+    info = torch.iinfo(qdtype)
+    g = torch.Generator("cpu").manual_seed(b)
+    q = torch.randint(info.min, info.max, shape, generator=g, dtype=qdtype)
+    got = torch.ops.fxpr.fixed_row_sum(q.to(DEV), b).cpu()
+    want = N.fixed_row_sum(q.numpy(), b)
+    assert got.shape == tuple(shape[:-1])
+    assert np.array_equal(got.numpy(), want)
+
+
+def test_row_sum_reference_kats():
+    # fxpr_vllm/_tests/test_sum.py:50-119 through float_to_fixed + fixed_row_sum
+    k = KATS["sum_on_q_grid"]
+    q = torch.tensor(k["q_i32"], dtype=torch.int32, device=DEV)
+    x = torch.ops.fxpr.fixed_to_float(q.to(torch.int64), 32, 16)
+    s = torch.ops.fxpr.fixed_row_sum(torch.ops.fxpr.float_to_fixed(x, 32, 16), 32)
+    assert s.item() == k["sum_q"]
+    assert torch.equal(x.sum().reshape(1).view(torch.int32).cpu(),
+                       torch.ops.fxpr.fixed_to_float(s.to(torch.int64), 32, 16).reshape(1).view(torch.int32).cpu())
+    for name in ("sum_saturates_max", "sum_saturates_min"):
+        k = KATS[name]
+        q = torch.ops.fxpr.float_to_fixed(torch.tensor(k["x_f32"], device=DEV), 32, 16)
+        assert torch.ops.fxpr.fixed_row_sum(q, 32).item() == k["sum_q"]
+    k = KATS["sum_associativity"]
+    a = torch.ops.fxpr.fixed_row_sum(torch.ops.fxpr.float_to_fixed(torch.tensor(k["order_a"], device=DEV), 64, 16), 64)
+    b = torch.ops.fxpr.fixed_row_sum(torch.ops.fxpr.float_to_fixed(torch.tensor(k["order_b"], device=DEV), 64, 16), 64)
+    assert a.item() == b.item()
+    assert torch.ops.fxpr.fixed_to_float(a, 32, 16).item() == k["sum_f32"]
+
+
+def test_row_sum_empty():
+    assert torch.ops.fxpr.fixed_row_sum(torch.empty(3, 0, dtype=torch.int32, device=DEV), 32).tolist() == [0, 0, 0]
+    assert torch.ops.fxpr.fixed_row_sum(torch.empty(0, 4, dtype=torch.int32, device=DEV), 32).shape == (0,)
+
+
+# --------------------------------------------------------------------------
+# RMSNorm
+
+
+def _rms_case(io_dtype, shape, seed, residual):
+    x = seeded(shape, seed, dtype=io_dtype)
+    w = seeded(shape[-1:], seed + 1, std=0.1, mean=1.0, dtype=io_dtype)
+    r = seeded(shape, seed + 2, dtype=io_dtype) if residual else None
+    return x, w, r
+
+
+def _rms_check(x, w, r, b, f, eps=1e-6):
+    io = IO_NAME[x.dtype]
+    xd, wd = x.to(DEV), w.to(DEV)
+    rd = r.to(DEV).clone() if r is not None else None
+    if rd is None:
+        y = K.rms_norm_fxp_run(xd, wd, eps, int_bits=b, frac_bits=f)
+    else:
+        y = K.rms_norm_fxp_residual_run(xd, rd, wd, eps, int_bits=b, frac_bits=f)
+    y_want, r_want = R.rms_norm(to_np(x), to_np(w), eps, io, b, f,
+                                residual=None if r is None else to_np(r))
+    y_want = from_np(y_want, x.dtype)
+    assert nan_aware_equal(y.cpu(), y_want), mismatch_report(y.cpu(), y_want)
+    if r is not None:
+        r_want = from_np(r_want, x.dtype)
+        assert nan_aware_equal(rd.cpu(), r_want), mismatch_report(rd.cpu(), r_want)
+    return y
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("residual", [False, True])
+@pytest.mark.parametrize("b,f", BITS)
+@pytest.mark.parametrize("shape", [(64, 4096), (3, 7), (1, 1), (2, 40_000), (17, 1000)])
+def test_rms_norm_bit_exact(dtype, residual, b, f, shape):
+    x, w, r = _rms_case(dtype, shape, seed=hash((shape, b)) % 1000, residual=residual)
+    _rms_check(x, w, r, b, f)
+
+
+def test_rms_norm_op_uses_runtime_config(monkeypatch):
+    x, w, r = _rms_case(torch.bfloat16, (8, 4096), 5, True)
+    for b, f in ((32, 16), (64, 32)):
+        monkeypatch.setenv("FXPR_INT_BITS", str(b))
+        monkeypatch.setenv("FXPR_FRAC_BITS", str(f))
+        fxpr_config.reset_runtime_config()
+        try:
+            rd = r.to(DEV).clone()
+            y = torch.ops.fxpr.rms_norm_fxp_residual(x.to(DEV), rd, w.to(DEV), 1e-6)
+            y_want, r_want = R.rms_norm(to_np(x), to_np(w), 1e-6, "bf16", b, f, residual=to_np(r))
+            assert torch.equal(y.cpu(), from_np(y_want, torch.bfloat16))
+            assert torch.equal(rd.cpu(), from_np(r_want, torch.bfloat16))
+            y2 = torch.ops.fxpr.rms_norm_fxp(x.to(DEV), w.to(DEV), 1e-6)
+            assert torch.equal(y2.cpu(), from_np(R.rms_norm(to_np(x), to_np(w), 1e-6, "bf16", b, f)[0],
+                                                 torch.bfloat16))
+        finally:
+            fxpr_config.reset_runtime_config()
+
+
+def test_rms_norm_noncontiguous_residual_copy_back():
+    x, w, _ = _rms_case(torch.float16, (6, 64), 9, False)
+    base = seeded((64, 6), 10, dtype=torch.float16)
+    r_nc = base.to(DEV).t()  # [6, 64] non-contiguous view
+    r_host = base.t().contiguous()
+    y = torch.ops.fxpr.rms_norm_fxp_residual(x.to(DEV), r_nc, w.to(DEV), 1e-6)
+    y_want, r_want = R.rms_norm(to_np(x), to_np(w), 1e-6, "f16", 32, 16, residual=to_np(r_host))
+    assert torch.equal(y.cpu(), from_np(y_want, torch.float16))
+    assert torch.equal(r_nc.cpu(), from_np(r_want, torch.float16))
+
+
+def test_rms_norm_batch_invariance():
+    x, w, r = _rms_case(torch.bfloat16, (128, 4096), 21, True)
+    xd, wd = x.to(DEV), w.to(DEV)
+    full = K.rms_norm_fxp_run(xd, wd, 1e-6, 32, 16)
+    for row in (0, 3, 17, 64, 127):
+        for batch in (1, 4, 16, 128):
+            if row >= batch:
+                continue
+            sub = xd[:batch].clone()
+            out = K.rms_norm_fxp_run(sub, wd, 1e-6, 32, 16)
+            assert torch.equal(out[row], full[row])
+
+
+@pytest.mark.parametrize("shape", [(2, 7), (3, 16), (4, 31)])
+def test_reference_rms_norm_correctness(shape):
+    # fxpr_vllm/_tests/test_rms_norm.py:39-57
+    g = torch.Generator("cpu").manual_seed(0)
+    x = ((torch.rand(shape, generator=g) - 0.5) * 32.0).to(DEV)
+    w = ((torch.rand(shape[1:], generator=g) - 0.5) * 4.0).to(DEV)
+    got = torch.ops.fxpr.rms_norm_fxp(x, w, 1e-6)
+    ref = x * w * (1.0 / torch.sqrt((x * x).mean(dim=-1, keepdim=True) + 1e-6))
+    assert torch.allclose(got, ref, atol=5e-4, rtol=5e-4)
+
+
+_TOL = {torch.float32: 5e-4, torch.float16: 5e-3, torch.bfloat16: 2e-2}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_reference_rms_norm_residual_native_dtype(dtype):
+    # fxpr_vllm/_tests/test_rms_norm.py:100-130
+    g = torch.Generator("cpu").manual_seed(11)
+    x = ((torch.rand((4, 32), generator=g) - 0.5) * 2.0).to(dtype).to(DEV)
+    r = ((torch.rand((4, 32), generator=g) - 0.5) * 2.0).to(dtype).to(DEV)
+    w = ((torch.rand((32,), generator=g) - 0.5) * 2.0).to(dtype).to(DEV)
+    r_orig = r.clone()
+    out = torch.ops.fxpr.rms_norm_fxp_residual(x, r, w, 1e-6)
+    assert out.dtype == dtype and r.dtype == dtype
+    expected_r = (x.float() + r_orig.float()).to(dtype)
+    tol = _TOL[dtype]
+    assert torch.allclose(r.float(), expected_r.float(), atol=tol, rtol=tol)
+
+
+def test_reference_rms_norm_associativity():
+    # fxpr_vllm/_tests/test_rms_norm.py:133-151
+    k = KATS["rms_norm_associativity"]
+    xa = torch.tensor(k["x_f32"], device=DEV)
+    perm = torch.tensor(k["perm"], device=DEV)
+    x = torch.stack([xa, xa[perm]])
+    y = torch.ops.fxpr.rms_norm_fxp(x, torch.ones(5, device=DEV), k["eps"])
+    assert torch.equal(y[1], y[0][perm])
+
+
+def test_rms_norm_errors_and_empty():
+    x = torch.ones(2, 8, device=DEV)
+    with pytest.raises(TypeError):
+        torch.ops.fxpr.rms_norm_fxp(x, torch.ones(8, device=DEV, dtype=torch.float16), 1e-6)
+    with pytest.raises(TypeError):
+        torch.ops.fxpr.rms_norm_fxp(x.double(), torch.ones(8, device=DEV).double(), 1e-6)
+    with pytest.raises(ValueError):
+        torch.ops.fxpr.rms_norm_fxp_residual(x, torch.ones(3, 8, device=DEV), torch.ones(8, device=DEV), 1e-6)
+    e = torch.ops.fxpr.rms_norm_fxp(torch.empty(0, 8, device=DEV), torch.ones(8, device=DEV), 1e-6)
+    assert e.shape == (0, 8)
+
+
+def test_rms_norm_run_to_run():
+    x, w, _ = _rms_case(torch.bfloat16, (512, 4096), 31, False)
+    xd, wd = x.to(DEV), w.to(DEV)
+    a = torch.ops.fxpr.rms_norm_fxp(xd, wd, 1e-6)
+    for _ in range(3):
+        assert torch.equal(a, torch.ops.fxpr.rms_norm_fxp(xd, wd, 1e-6))
+
+
+# --------------------------------------------------------------------------
+# log-softmax
+
+
+def _logits(rows, vocab, seed, dtype=torch.bfloat16):
+    """~N(0, 4^2) with 1% outliers at +-30 (the bandwidth config's data)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    x = torch.randn(rows, vocab, generator=g) * 4.0
+    mask = torch.rand(rows, vocab, generator=g) < 0.01
+    sign = torch.where(torch.rand(rows, vocab, generator=g) < 0.5, -1.0, 1.0)
+    x = torch.where(mask, 30.0 * sign, x)
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("b,f", [(32, 16), (64, 32), (16, 8)])
+@pytest.mark.parametrize("out_dtype", [None, torch.float32])
+def test_log_softmax_vocab_bit_exact(b, f, out_dtype):
+    x = _logits(4, 128_256, seed=b + f)
+    got = torch.ops.fxpr.log_softmax_fxp(x.to(DEV), b, f, out_dtype).cpu()
+    want = from_np(R.log_softmax(to_np(x), "bf16", IO_NAME[out_dtype or x.dtype], b, f), out_dtype or x.dtype)
+    assert nan_aware_equal(got, want), mismatch_report(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(1, 1), (5, 7), (3, 1000), (2, 300_001), (33, 4096)])
+def test_log_softmax_shapes_bit_exact(dtype, shape):
+    x = _logits(*shape, seed=shape[1], dtype=dtype)
+    got = torch.ops.fxpr.log_softmax_fxp(x.to(DEV), 32, 16).cpu()
+    want = from_np(R.log_softmax(to_np(x), IO_NAME[dtype], IO_NAME[dtype], 32, 16), dtype)
+    assert nan_aware_equal(got, want), mismatch_report(got, want)
+
+
+def test_log_softmax_special_rows():
+    x = torch.tensor([[-float("inf")] * 8, [float("nan"), 0, 1, 2, 3, 4, 5, 6],
+                      [0, -float("inf"), 1, -float("inf"), 2, 3, 4, 5]], dtype=torch.float32)
+    got = torch.ops.fxpr.log_softmax_fxp(x.to(DEV), 32, 16).cpu()
+    want = torch.from_numpy(R.log_softmax(x.numpy(), "f32", "f32", 32, 16))
+    assert nan_aware_equal(got, want)
+
+
+def test_log_softmax_close_to_torch():
+    x = _logits(16, 32_000, seed=4, dtype=torch.float32)
+    got = torch.ops.fxpr.log_softmax_fxp(x.to(DEV), 64, 32).cpu()
+    ref = torch.log_softmax(x.double(), dim=-1)
+    assert torch.allclose(got.double(), ref, atol=1e-4, rtol=1e-5)
+
+
+def test_log_softmax_batch_and_run_invariance():
+    x = _logits(64, 128_256, seed=8).to(DEV)
+    full = torch.ops.fxpr.log_softmax_fxp(x, 32, 16)
+    for row in (0, 5, 63):
+        assert torch.equal(torch.ops.fxpr.log_softmax_fxp(x[row:row + 1].clone(), 32, 16)[0], full[row])
+    assert torch.equal(full, torch.ops.fxpr.log_softmax_fxp(x, 32, 16))

@@ -1,0 +1,96 @@
+"""Build libfxpr_hip.so (the gfx950 kernels + C ABI) in-tree with hipcc.
+
+    python build.py [--jobs N] [--verbose]
+
+Each csrc/*.hip file is compiled to an object under _build/ and the objects
+are linked into fxpr_vllm/libfxpr_hip.so, which fxpr_vllm/_hip.py loads with
+ctypes. hipcc cross-compiles for gfx950, so this works without a GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+REPO = HERE.parent
+CSRC = HERE / "csrc"
+BUILD = HERE / "_build"
+OUT = HERE / "fxpr_vllm" / "libfxpr_hip.so"
+ARCH = os.environ.get("FXPR_OFFLOAD_ARCH", "gfx950")
+
+# -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32.
+# -ffp-contract=off: no fused multiply-add, so every fp32 operation rounds on
+# its own exactly like the CPU restatement.
+COMMON_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    f"--offload-arch={ARCH}",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+    f"-I{REPO / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; install ROCm or put hipcc on PATH")
+    return path
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd[:4])} ...")
+    # the host pass warns that it does not know the packed-fp32 feature
+    noise = "packed-fp32-ops"
+    for line in (res.stderr or "").splitlines():
+        if verbose and noise not in line:
+            print(line)
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    BUILD.mkdir(exist_ok=True)
+    cc = hipcc()
+    objs = [BUILD / (s.stem + ".o") for s in sources]
+    jobs = jobs or min(8, len(sources))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [
+            ex.submit(_run, [cc, *COMMON_FLAGS, "-c", str(s), "-o", str(o)], verbose)
+            for s, o in zip(sources, objs)
+        ]
+        for f in futs:
+            f.result()
+    tmp = OUT.with_suffix(".so.tmp")
+    _run([cc, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp)],
+         verbose)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--verbose", action="store_true")
+    args = ap.parse_args()
+    out = build(args.jobs, args.verbose)
+    print(f"built {out}")
+
+
+if __name__ == "__main__":
+    main()

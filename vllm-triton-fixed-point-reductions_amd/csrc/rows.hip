@@ -1,0 +1,419 @@
+// Row reductions with integer (fixed-point) accumulation: row sum, RMSNorm
+// (+fused residual) and log-softmax.
+//
+// One workgroup owns one row, so a row never depends on its neighbours
+// (batch invariance). Within the row every partial is an integer and the
+// cross-lane / cross-wave combine is an exact (or, for non-negative terms,
+// saturating-and-therefore-associative) integer sum, so the bits do not
+// depend on the workgroup size or the reduction tree either. Rows are
+// streamed with 16-byte vector loads and, up to NREG vectors per thread, kept
+// in registers between the reduction pass and the output pass so x is read
+// from HBM once.
+
+#include "fxp_device.h"
+#include "fxpr_internal.h"
+
+namespace fxpr {
+namespace {
+
+template <typename T, int N> struct alignas(sizeof(T) * N) Vec { T v[N]; };
+
+constexpr int kMaxThreads = 1024;
+
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return (a != a || a > b) ? a : b;  // NaN wins, otherwise the larger value
+}
+
+__device__ float block_max(float v, float* smem) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max_nan(v, __shfl_xor(v, o, 64));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) smem[wave] = v;
+  __syncthreads();
+  float r = smem[0];
+  for (int w = 1; w < nw; ++w) r = max_nan(r, smem[w]);
+  return r;
+}
+
+__device__ uint64_t block_sat_sum(uint64_t v, uint64_t qmax, uint64_t* smem) {
+  v = wave_sat_sum(v, qmax);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) smem[wave] = v;
+  __syncthreads();
+  uint64_t r = smem[0];
+  for (int w = 1; w < nw; ++w) r = sat_add_nonneg(r, smem[w], qmax);
+  return r;
+}
+
+template <int BITS> __device__ __forceinline__ uint64_t quant_nonneg(float s) {
+  // s >= 0 or NaN, so the result is in [0, qmax]
+  return static_cast<uint64_t>(quant<BITS>(s));
+}
+
+// ---------------------------------------------------------------------------
+// Exact integer row sum, saturated once to OBITS.
+
+template <int QBITS> struct RowSumTypes;
+template <> struct RowSumTypes<16> { using Q = int16_t; using Acc = int64_t; };
+template <> struct RowSumTypes<32> { using Q = int32_t; using Acc = int64_t; };
+template <> struct RowSumTypes<64> { using Q = int64_t; using Acc = __int128; };
+
+__device__ __forceinline__ int64_t shfl_xor_i64(int64_t v, int o) { return __shfl_xor(v, o, 64); }
+__device__ __forceinline__ __int128 shfl_xor_i128(__int128 v, int o) {
+  uint64_t lo = static_cast<uint64_t>(v), hi = static_cast<uint64_t>(v >> 64);
+  lo = __shfl_xor(lo, o, 64);
+  hi = __shfl_xor(hi, o, 64);
+  return static_cast<__int128>((static_cast<unsigned __int128>(hi) << 64) | lo);
+}
+
+template <int QBITS, int OBITS>
+__global__ __launch_bounds__(256) void row_sum_kernel(
+    const typename RowSumTypes<QBITS>::Q* __restrict__ q, void* __restrict__ out, int64_t cols) {
+  using Acc = typename RowSumTypes<QBITS>::Acc;
+  __shared__ Acc smem[4];
+  const int64_t row = blockIdx.x;
+  const auto* p = q + row * cols;
+  Acc acc = 0;
+  for (int64_t j = threadIdx.x; j < cols; j += 256) acc += static_cast<Acc>(p[j]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    if constexpr (QBITS == 64) acc += shfl_xor_i128(acc, o);
+    else acc += shfl_xor_i64(acc, o);
+  }
+  if ((threadIdx.x & 63) == 0) smem[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Acc t = smem[0] + smem[1] + smem[2] + smem[3];
+    const Acc hi = static_cast<Acc>((uint64_t(1) << (OBITS - 1)) - 1);
+    const Acc lo = -hi - 1;
+    t = t > hi ? hi : (t < lo ? lo : t);
+    if constexpr (OBITS == 16) static_cast<int16_t*>(out)[row] = static_cast<int16_t>(t);
+    else if constexpr (OBITS == 32) static_cast<int32_t*>(out)[row] = static_cast<int32_t>(t);
+    else static_cast<int64_t*>(out)[row] = static_cast<int64_t>(t);
+  }
+}
+
+template <int QBITS>
+int launch_row_sum(const void* q, void* out, int obits, int64_t rows, int64_t cols, hipStream_t st) {
+  using Q = typename RowSumTypes<QBITS>::Q;
+  const Q* qp = static_cast<const Q*>(q);
+  dim3 grid(static_cast<unsigned>(rows));
+  switch (obits) {
+    case 16: row_sum_kernel<QBITS, 16><<<grid, 256, 0, st>>>(qp, out, cols); break;
+    case 32: row_sum_kernel<QBITS, 32><<<grid, 256, 0, st>>>(qp, out, cols); break;
+    default: row_sum_kernel<QBITS, 64><<<grid, 256, 0, st>>>(qp, out, cols); break;
+  }
+  return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm(+residual).
+//
+// Pass 1 (per element j of the row): v = fl32(x) [+ fl32(r)]; with a residual
+// store r <- IO(v); add float_to_fixed(fl32(v*v)) to a saturating unsigned
+// accumulator. Row total T (exact sum clamped to qmax).
+// rrms = 1 / sqrt(fl32(T) * 2^-f / H + eps).
+// Pass 2: u = fl32(IO(v)) (what was stored) or fl32(x); y = IO((u * w) * rrms).
+
+template <int DT, int VEC, int NREG, int BITS, bool RES>
+__global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
+    const typename Io<DT>::T* __restrict__ x, typename Io<DT>::T* __restrict__ r,
+    const typename Io<DT>::T* __restrict__ w, typename Io<DT>::T* __restrict__ y,
+    int64_t hidden, float eps, float scale, float inv_scale, uint64_t qmax) {
+  using T = typename Io<DT>::T;
+  using V = Vec<T, VEC>;
+  __shared__ uint64_t red[kMaxThreads / 64];
+
+  const int64_t row = blockIdx.x;
+  const int64_t nchunks = hidden / VEC;
+  const int nthr = blockDim.x;
+  const int tid = threadIdx.x;
+  const V* xr = reinterpret_cast<const V*>(x + row * hidden);
+  V* rr = reinterpret_cast<V*>(r + row * hidden);
+  const V* wr = reinterpret_cast<const V*>(w);
+  V* yr = reinterpret_cast<V*>(y + row * hidden);
+
+  float keep[NREG][VEC];
+  uint64_t acc = 0;
+
+  auto pass1 = [&](int64_t c, float (&u)[VEC]) {
+    V xv = xr[c];
+    float v[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) v[j] = Io<DT>::load(xv.v[j]);
+    if constexpr (RES) {
+      V rv = rr[c];
+      V sv;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        v[j] = __fadd_rn(v[j], Io<DT>::load(rv.v[j]));
+        sv.v[j] = Io<DT>::store(v[j]);
+        u[j] = Io<DT>::load(sv.v[j]);
+      }
+      rr[c] = sv;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) u[j] = v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < VEC; ++j)
+      acc = sat_add_nonneg(acc, quant_nonneg<BITS>(__fmul_rn(__fmul_rn(v[j], v[j]), scale)), qmax);
+  };
+
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+    if (c < nchunks) pass1(c, keep[i]);
+  }
+  for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) {
+    float u[VEC];
+    pass1(c, u);
+  }
+
+  const uint64_t total = block_sat_sum(acc, qmax, red);
+  float ms = __fdiv_rn(fixed_to_f32(static_cast<int64_t>(total), inv_scale), static_cast<float>(hidden));
+  ms = ms > 0.0f ? ms : 0.0f;
+  const float rrms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+
+  auto pass2 = [&](int64_t c, const float (&u)[VEC]) {
+    V wv = wr[c];
+    V yv;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j)
+      yv.v[j] = Io<DT>::store(__fmul_rn(__fmul_rn(u[j], Io<DT>::load(wv.v[j])), rrms));
+    yr[c] = yv;
+  };
+
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+    if (c < nchunks) pass2(c, keep[i]);
+  }
+  for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) {
+    V src = RES ? rr[c] : xr[c];  // residual already holds IO(v)
+    float u[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) u[j] = Io<DT>::load(src.v[j]);
+    pass2(c, u);
+  }
+}
+
+inline int threads_for(int64_t nchunks, int per_thread) {
+  int64_t t = cdiv(nchunks, per_thread);
+  t = cdiv(t, 64) * 64;
+  if (t < 64) t = 64;
+  if (t > kMaxThreads) t = kMaxThreads;
+  return static_cast<int>(t);
+}
+
+template <int DT, int VEC, int BITS>
+int launch_rms_bits(const void* x, void* r, const void* w, void* y, int64_t rows, int64_t hidden,
+                    float eps, float scale, float inv, uint64_t qmax, hipStream_t st) {
+  using T = typename Io<DT>::T;
+  constexpr int NREG = 4;
+  const int64_t nchunks = hidden / VEC;
+  const int nthr = threads_for(nchunks, 2);
+  dim3 grid(static_cast<unsigned>(rows));
+  if (r)
+    rms_norm_kernel<DT, VEC, NREG, BITS, true><<<grid, nthr, 0, st>>>(
+        static_cast<const T*>(x), static_cast<T*>(r), static_cast<const T*>(w), static_cast<T*>(y),
+        hidden, eps, scale, inv, qmax);
+  else
+    rms_norm_kernel<DT, VEC, NREG, BITS, false><<<grid, nthr, 0, st>>>(
+        static_cast<const T*>(x), nullptr, static_cast<const T*>(w), static_cast<T*>(y),
+        hidden, eps, scale, inv, qmax);
+  return launch_status();
+}
+
+template <int DT>
+int launch_rms(const void* x, void* r, const void* w, void* y, int64_t rows, int64_t hidden,
+               float eps, int bits, int frac, hipStream_t st) {
+  using T = typename Io<DT>::T;
+  constexpr int VEC = 16 / sizeof(T);
+  const float scale = pow2f(frac), inv = pow2f(-frac);
+  const uint64_t qmax = qmax_for_bits(bits);
+  const bool vec_ok = hidden % VEC == 0 && aligned(x, 16) && aligned(w, 16) && aligned(y, 16) &&
+                      (!r || aligned(r, 16));
+#define FXPR_RMS_CASE(V, B) \
+  return launch_rms_bits<DT, V, B>(x, r, w, y, rows, hidden, eps, scale, inv, qmax, st)
+  if (vec_ok) {
+    if (bits == 16) FXPR_RMS_CASE(VEC, 16);
+    if (bits == 32) FXPR_RMS_CASE(VEC, 32);
+    FXPR_RMS_CASE(VEC, 64);
+  } else {
+    if (bits == 16) FXPR_RMS_CASE(1, 16);
+    if (bits == 32) FXPR_RMS_CASE(1, 32);
+    FXPR_RMS_CASE(1, 64);
+  }
+#undef FXPR_RMS_CASE
+}
+
+// ---------------------------------------------------------------------------
+// Log-softmax.
+//
+// Pass 1: m = max_j fl32(x_j) (NaN propagates).
+// Pass 2: S = sat-sum_j RNE_sat(exp_scaled(fl32(x_j) - m, f)).
+// lse = m + ln(fl32(S) * 2^-f) (ln by log_own; S == 0 gives -inf).
+// Pass 3: y_j = OUT(fl32(x_j) - lse).
+
+template <int XDT, int YDT, int VEC, int NREG, int BITS>
+__global__ __launch_bounds__(kMaxThreads) void log_softmax_kernel(
+    const typename Io<XDT>::T* __restrict__ x, typename Io<YDT>::T* __restrict__ y, int64_t cols,
+    int frac, float inv_scale, uint64_t qmax) {
+  using XT = typename Io<XDT>::T;
+  using YT = typename Io<YDT>::T;
+  using XV = Vec<XT, VEC>;
+  using YV = Vec<YT, VEC>;
+  __shared__ float fred[kMaxThreads / 64];
+  __shared__ uint64_t ired[kMaxThreads / 64];
+
+  const int64_t row = blockIdx.x;
+  const int64_t nchunks = cols / VEC;
+  const int nthr = blockDim.x;
+  const int tid = threadIdx.x;
+  const XV* xr = reinterpret_cast<const XV*>(x + row * cols);
+  YV* yr = reinterpret_cast<YV*>(y + row * cols);
+
+  XV keep[NREG];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+    if (c < nchunks) {
+      keep[i] = xr[c];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) m = max_nan(m, Io<XDT>::load(keep[i].v[j]));
+    }
+  }
+  for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) {
+    XV xv = xr[c];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) m = max_nan(m, Io<XDT>::load(xv.v[j]));
+  }
+  m = block_max(m, fred);
+
+  uint64_t acc = 0;
+  auto accum = [&](const XV& xv) {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
+      acc = sat_add_nonneg(acc, quant_nonneg<BITS>(exp_scaled(d, frac)), qmax);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+    if (c < nchunks) accum(keep[i]);
+  }
+  for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum(xr[c]);
+  const uint64_t total = block_sat_sum(acc, qmax, ired);
+
+  const float lnS = total == 0 ? -__builtin_inff()
+                               : log_own(fixed_to_f32(static_cast<int64_t>(total), inv_scale));
+  const float lse = __fadd_rn(m, lnS);
+
+  auto emit = [&](int64_t c, const XV& xv) {
+    YV yv;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) yv.v[j] = Io<YDT>::store(__fsub_rn(Io<XDT>::load(xv.v[j]), lse));
+    yr[c] = yv;
+  };
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+    if (c < nchunks) emit(c, keep[i]);
+  }
+  for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) emit(c, xr[c]);
+}
+
+template <int XDT, int YDT, int VEC>
+int launch_lsm_vec(const void* x, void* y, int64_t rows, int64_t cols, int bits, int frac,
+                   hipStream_t st) {
+  using XT = typename Io<XDT>::T;
+  using YT = typename Io<YDT>::T;
+  constexpr int NREG = VEC == 1 ? 8 : 16;
+  const int64_t nchunks = cols / VEC;
+  const int nthr = threads_for(nchunks, NREG);
+  const float inv = pow2f(-frac);
+  const uint64_t qmax = qmax_for_bits(bits);
+  dim3 grid(static_cast<unsigned>(rows));
+  const XT* xp = static_cast<const XT*>(x);
+  YT* yp = static_cast<YT*>(y);
+  if (bits == 16)
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 16><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax);
+  else if (bits == 32)
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 32><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax);
+  else
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 64><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax);
+  return launch_status();
+}
+
+template <int XDT, int YDT>
+int launch_lsm(const void* x, void* y, int64_t rows, int64_t cols, int bits, int frac, hipStream_t st) {
+  using XT = typename Io<XDT>::T;
+  using YT = typename Io<YDT>::T;
+  constexpr int VEC = 16 / sizeof(XT);
+  if (cols % VEC == 0 && aligned(x, 16) && aligned(y, sizeof(YT) * VEC))
+    return launch_lsm_vec<XDT, YDT, VEC>(x, y, rows, cols, bits, frac, st);
+  return launch_lsm_vec<XDT, YDT, 1>(x, y, rows, cols, bits, frac, st);
+}
+
+}  // namespace
+}  // namespace fxpr
+
+using namespace fxpr;
+
+extern "C" int fxpr_fixed_row_sum(const void* q, int q_dtype, void* out, int int_bits,
+                                  int64_t rows, int64_t cols, void* stream) {
+  if (!valid_int_bits(int_bits)) return FXPR_E_BITS;
+  if (rows < 0 || cols < 0 || rows > 0x7fffffff) return FXPR_E_SHAPE;
+  if (rows == 0) return FXPR_OK;
+  if (!q || !out) return FXPR_E_ARG;
+  hipStream_t st = as_stream(stream);
+  switch (q_dtype) {
+    case FXPR_DTYPE_I16: return launch_row_sum<16>(q, out, int_bits, rows, cols, st);
+    case FXPR_DTYPE_I32: return launch_row_sum<32>(q, out, int_bits, rows, cols, st);
+    case FXPR_DTYPE_I64: return launch_row_sum<64>(q, out, int_bits, rows, cols, st);
+    default: return FXPR_E_DTYPE;
+  }
+}
+
+extern "C" int fxpr_rms_norm(const void* x, void* residual, const void* weight, void* y,
+                             int io_dtype, int64_t rows, int64_t hidden, float eps, int int_bits,
+                             int frac_bits, void* stream) {
+  if (!valid_int_bits(int_bits) || frac_bits < 0 || frac_bits > 63) return FXPR_E_BITS;
+  if (rows < 0 || hidden < 0 || rows > 0x7fffffff) return FXPR_E_SHAPE;
+  if (rows == 0 || hidden == 0) return FXPR_OK;
+  if (!x || !weight || !y) return FXPR_E_ARG;
+  hipStream_t st = as_stream(stream);
+  switch (io_dtype) {
+    case FXPR_DTYPE_F16: return launch_rms<FXPR_DTYPE_F16>(x, residual, weight, y, rows, hidden, eps, int_bits, frac_bits, st);
+    case FXPR_DTYPE_BF16: return launch_rms<FXPR_DTYPE_BF16>(x, residual, weight, y, rows, hidden, eps, int_bits, frac_bits, st);
+    case FXPR_DTYPE_F32: return launch_rms<FXPR_DTYPE_F32>(x, residual, weight, y, rows, hidden, eps, int_bits, frac_bits, st);
+    default: return FXPR_E_DTYPE;
+  }
+}
+
+extern "C" int fxpr_log_softmax(const void* x, int x_dtype, void* y, int y_dtype, int64_t rows,
+                                int64_t cols, int int_bits, int frac_bits, void* stream) {
+  if (!valid_int_bits(int_bits) || frac_bits < 0 || frac_bits > 63) return FXPR_E_BITS;
+  if (rows < 0 || cols < 0 || rows > 0x7fffffff) return FXPR_E_SHAPE;
+  if (rows == 0 || cols == 0) return FXPR_OK;
+  if (!x || !y) return FXPR_E_ARG;
+  hipStream_t st = as_stream(stream);
+  const bool f32_out = y_dtype == FXPR_DTYPE_F32;
+  if (!f32_out && y_dtype != x_dtype) return FXPR_E_DTYPE;
+  switch (x_dtype) {
+    case FXPR_DTYPE_F16:
+      return f32_out ? launch_lsm<FXPR_DTYPE_F16, FXPR_DTYPE_F32>(x, y, rows, cols, int_bits, frac_bits, st)
+                     : launch_lsm<FXPR_DTYPE_F16, FXPR_DTYPE_F16>(x, y, rows, cols, int_bits, frac_bits, st);
+    case FXPR_DTYPE_BF16:
+      return f32_out ? launch_lsm<FXPR_DTYPE_BF16, FXPR_DTYPE_F32>(x, y, rows, cols, int_bits, frac_bits, st)
+                     : launch_lsm<FXPR_DTYPE_BF16, FXPR_DTYPE_BF16>(x, y, rows, cols, int_bits, frac_bits, st);
+    case FXPR_DTYPE_F32:
+      return launch_lsm<FXPR_DTYPE_F32, FXPR_DTYPE_F32>(x, y, rows, cols, int_bits, frac_bits, st);
+    default: return FXPR_E_DTYPE;
+  }
+}

@@ -1,0 +1,97 @@
+"""torch.ops.fxpr.* schemas and their "CUDA"-key impls (HIP kernels).
+
+The six reference schemas are kept verbatim (fxpr_vllm/_lib.py:13-33 of the
+reference) so callers and torch.compile graphs are a drop-in; PyTorch-ROCm
+dispatches HIP tensors through the CUDA key. Two schemas are new in this
+build: fixed_row_sum (the integer sum the reference's tests do with torch,
+_tests/test_sum.py:12-16) and log_softmax_fxp (listed in the reference
+README.md:60 but not shipped). Validation and error classes follow the
+reference impls (_lib.py:36-129).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ._kernels import casts as _casts
+from ._kernels import rows as _rows
+
+_lib = torch.library.Library("fxpr", "DEF")
+
+_lib.define("float_to_fixed(Tensor x, int int_bits, int fxp_frac_bits) -> Tensor")
+_lib.define("fixed_to_float(Tensor x, int float_bits, int fxp_frac_bits) -> Tensor")
+# RMSNorm takes its fixed-point format from FXPR_INT_BITS / FXPR_FRAC_BITS.
+_lib.define("rms_norm_fxp(Tensor x, Tensor weight_fp32, float eps) -> Tensor")
+_lib.define(
+    "rms_norm_fxp_residual(Tensor x, Tensor(a!) residual, Tensor weight_fp32, "
+    "float eps) -> Tensor"
+)
+_lib.define(
+    "gemm_fxp(Tensor a, Tensor b, Tensor? bias, int fxp_int_bits, "
+    "int fxp_frac_bits) -> Tensor"
+)
+_lib.define(
+    "unified_attention_fxp(Tensor q, Tensor kv_cache, Tensor(a!) o, "
+    "Tensor query_start_loc, Tensor seq_lens, Tensor block_table, "
+    "int max_query_len, Tensor? alibi_slopes, bool is_causal, "
+    "float? softmax_scale, int fxp_int_bits, int fxp_frac_bits, "
+    "float logit_softcap, int window_size, int num_kv_splits) -> ()"
+)
+_lib.define("fixed_row_sum(Tensor q, int int_bits) -> Tensor")
+_lib.define(
+    "log_softmax_fxp(Tensor x, int fxp_int_bits, int fxp_frac_bits, "
+    "ScalarType? out_dtype=None) -> Tensor"
+)
+
+
+def _check_frac_bits(n: int) -> None:
+    if int(n) not in (8, 16, 32):
+        raise ValueError(f"fxp_frac_bits must be 8/16/32, got {n}")
+
+
+def _check_int_bits(n: int) -> None:
+    if int(n) not in (16, 32, 64):
+        raise ValueError(f"int_bits must be 16/32/64, got {n}")
+
+
+def _float_to_fixed_cuda(x: torch.Tensor, int_bits: int, fxp_frac_bits: int):
+    _check_int_bits(int_bits)
+    _check_frac_bits(fxp_frac_bits)
+    return _casts.float_to_fixed_run(x, int(int_bits), int(fxp_frac_bits))
+
+
+def _fixed_to_float_cuda(x: torch.Tensor, float_bits: int, fxp_frac_bits: int):
+    if int(float_bits) not in (16, 32, 64):
+        raise ValueError(f"float_bits must be 16/32/64, got {float_bits}")
+    _check_frac_bits(fxp_frac_bits)
+    return _casts.fixed_to_float_run(x, int(float_bits), int(fxp_frac_bits))
+
+
+def _rms_norm_fxp_cuda(x: torch.Tensor, weight: torch.Tensor, eps: float):
+    return _rows.rms_norm_fxp_run(x, weight, float(eps))
+
+
+def _rms_norm_fxp_residual_cuda(x: torch.Tensor, residual: torch.Tensor,
+                                weight: torch.Tensor, eps: float):
+    return _rows.rms_norm_fxp_residual_run(x, residual, weight, float(eps))
+
+
+def _fixed_row_sum_cuda(q: torch.Tensor, int_bits: int):
+    _check_int_bits(int_bits)
+    return _rows.fixed_row_sum_run(q, int(int_bits))
+
+
+def _log_softmax_fxp_cuda(x: torch.Tensor, fxp_int_bits: int, fxp_frac_bits: int,
+                          out_dtype: torch.dtype | None = None):
+    _check_int_bits(fxp_int_bits)
+    _check_frac_bits(fxp_frac_bits)
+    return _rows.log_softmax_fxp_run(x, int(fxp_int_bits), int(fxp_frac_bits), out_dtype)
+
+
+# Register after definition so the functions stay importable by name.
+_lib.impl("float_to_fixed", _float_to_fixed_cuda, "CUDA")
+_lib.impl("fixed_to_float", _fixed_to_float_cuda, "CUDA")
+_lib.impl("rms_norm_fxp", _rms_norm_fxp_cuda, "CUDA")
+_lib.impl("rms_norm_fxp_residual", _rms_norm_fxp_residual_cuda, "CUDA")
+_lib.impl("fixed_row_sum", _fixed_row_sum_cuda, "CUDA")
+_lib.impl("log_softmax_fxp", _log_softmax_fxp_cuda, "CUDA")
