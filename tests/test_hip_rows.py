@@ -264,3 +264,17 @@ def test_log_softmax_batch_and_run_invariance():
     for row in (0, 5, 63):
         assert torch.equal(torch.ops.fxpr.log_softmax_fxp(x[row:row + 1].clone(), 32, 16)[0], full[row])
     assert torch.equal(full, torch.ops.fxpr.log_softmax_fxp(x, 32, 16))
+
+
+def test_rms_norm_rrms_correctly_rounded():
+    # 20k rows, each a different constant: every row exercises one IEEE
+    # sqrt + division on the device; a non-correctly-rounded sqrt or
+    # division shows up as ulp differences against the oracle
+    g = torch.Generator("cpu").manual_seed(123)
+    c = torch.exp(torch.rand(20_000, generator=g) * 12 - 6)
+    x = c[:, None].expand(20_000, 64).contiguous()
+    w = torch.ones(64)
+    for b, f in ((64, 32), (32, 16)):
+        y = K.rms_norm_fxp_run(x.to(DEV), w.to(DEV), 1e-6, int_bits=b, frac_bits=f).cpu()
+        want = torch.from_numpy(R.rms_norm(x.numpy(), w.numpy(), 1e-6, "f32", b, f)[0])
+        assert torch.equal(y, want), mismatch_report(y, want)

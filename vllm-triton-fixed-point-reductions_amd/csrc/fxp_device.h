@@ -12,6 +12,14 @@
 
 namespace fxpr {
 
+// Correctly rounded fp32 square root. HIP's __fsqrt_rn maps to the native
+// (approximate) v_sqrt_f32 unless OCML_BASIC_ROUNDED_OPERATIONS is defined;
+// the llvm.sqrt builtin gets the corrected IEEE sequence that hipcc emits by
+// default (-fhip-fp32-correctly-rounded-divide-sqrt). Plain `/` is likewise
+// the correctly rounded division.
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+__device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
+
 // ---------------------------------------------------------------------------
 // Storage types and conversions to / from fp32.
 
@@ -179,7 +187,7 @@ __device__ __forceinline__ float log_own(float y) {
     m = __fmul_rn(m, 0.5f);
     e += 1;
   }
-  float s = __fdiv_rn(__fsub_rn(m, 1.0f), __fadd_rn(m, 1.0f));
+  float s = div_rn(__fsub_rn(m, 1.0f), __fadd_rn(m, 1.0f));
   float z = __fmul_rn(s, s);
   float p = 0.111111111111111111f;                       // 1/9
   p = __fadd_rn(__fmul_rn(p, z), 0.142857142857142857f);  // 1/7

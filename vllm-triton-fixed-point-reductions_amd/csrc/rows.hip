@@ -173,9 +173,9 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
   }
 
   const uint64_t total = block_sat_sum(acc, qmax, red);
-  float ms = __fdiv_rn(fixed_to_f32(static_cast<int64_t>(total), inv_scale), static_cast<float>(hidden));
+  float ms = div_rn(fixed_to_f32(static_cast<int64_t>(total), inv_scale), static_cast<float>(hidden));
   ms = ms > 0.0f ? ms : 0.0f;
-  const float rrms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+  const float rrms = div_rn(1.0f, sqrt_rn(__fadd_rn(ms, eps)));
 
   auto pass2 = [&](int64_t c, const float (&u)[VEC]) {
     V wv = wr[c];
