@@ -1,0 +1,248 @@
+#!/usr/bin/env python
+"""Benchmark of the fxpr fixed-point kernels on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads a,b,...]
+
+Prints ONE JSON line. The headline (`metric`/`value`) is BASELINE.json's
+metric: the fixed-point lm_head GEMM in TFLOP/s (bf16 A[8192,4096] x
+B[4096,128256], Q16.16 in int32) whose `roofline` is against the dense bf16
+MFMA peak; the paged split-K decode attention (HBM GB/s and % of roofline),
+RMSNorm+residual and log-softmax lines ride along under `extra`, each with
+its own roofline. A step is one call of the workload's op on one batch of
+seeded synthetic input already resident in HBM; each workload times exactly K
+steps between HIP events recorded on the stream the kernels run on, after W
+warmup steps, with a device synchronize on both sides. Inputs whose total
+footprint would fit in the 256 MB MALL are rotated across copies so the
+figures are HBM figures.
+
+`cpu_baseline` times the numpy oracle (oracle/, the CPU restatement of the
+same fixed-point arithmetic) on a bounded sample of the headline workload on
+this box's host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG_ROOT = ROOT / "vllm-triton-fixed-point-reductions_amd"
+for _p in (str(PKG_ROOT), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+FP32_PEAK_TFLOPS = 157.3
+MALL_BYTES = 256 << 20
+
+METRIC = "fxp lm_head GEMM TFLOP/s; paged decode attn HBM GB/s (% of roofline)"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_op(fn, inputs, steps: int, warmup: int) -> float:
+    """Average ms per call over `steps` calls, rotating through `inputs`."""
+    import torch
+
+    for i in range(warmup):
+        fn(*inputs[i % len(inputs)])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(*inputs[i % len(inputs)])
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def copies_for(bytes_per_set: int) -> int:
+    """Input sets to rotate so one pass over them exceeds 2x the MALL."""
+    return max(1, min(8, -(-2 * MALL_BYTES // max(1, bytes_per_set))))
+
+
+def hbm_roofline(bytes_per_call: float, ms: float) -> dict:
+    gbs = bytes_per_call / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+
+
+def mfma_roofline(flops: float, ms: float, peak: float = BF16_PEAK_TFLOPS) -> dict:
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(tf / peak, 4), "traffic": None}
+
+
+# ---------------------------------------------------------------------------
+# workloads (each returns a dict; the synthetic data follows BASELINE.json)
+
+
+def wl_rms_norm(steps, warmup, int_bits=32, frac_bits=16, T=16384, H=4096):
+    import torch
+
+    from fxpr_vllm._kernels import rows as K
+
+    g = torch.Generator("cpu").manual_seed(0)
+    dev = "cuda"
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    r0 = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(H, generator=g) * 0.1 + 1.0).to(torch.bfloat16).to(dev)
+    nbytes = 4 * T * H * 2 + 2 * H
+    sets = [(x, r0.clone(), w) for _ in range(copies_for(nbytes))]
+
+    def fn(xx, rr, ww):
+        return K.rms_norm_fxp_residual_run(xx, rr, ww, 1e-6, int_bits=int_bits, frac_bits=frac_bits)
+
+    ms = time_op(fn, sets, steps, warmup)
+    return {"workload": f"rms_norm_residual bf16 [{T},{H}] Q{frac_bits}/i{int_bits}",
+            "ms": round(ms, 5), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms)}
+
+
+def _logits(R, V, seed=0):
+    import torch
+
+    g = torch.Generator("cpu").manual_seed(seed)
+    x = torch.randn(R, V, generator=g) * 4.0
+    mask = torch.rand(R, V, generator=g) < 0.01
+    sign = torch.where(torch.rand(R, V, generator=g) < 0.5, -1.0, 1.0)
+    return torch.where(mask, 30.0 * sign, x).to(torch.bfloat16)
+
+
+def wl_log_softmax(steps, warmup, int_bits=32, frac_bits=16, fp32_out=False, R=256, V=128256):
+    import torch
+
+    x = _logits(R, V).to("cuda")
+    out_dtype = torch.float32 if fp32_out else None
+    nbytes = R * V * (2 + (4 if fp32_out else 2))
+    sets = [(x.clone(),) for _ in range(copies_for(nbytes))]
+
+    def fn(xx):
+        return torch.ops.fxpr.log_softmax_fxp(xx, int_bits, frac_bits, out_dtype)
+
+    ms = time_op(fn, sets, steps, warmup)
+    return {"workload": f"log_softmax bf16 [{R},{V}] -> {'f32' if fp32_out else 'bf16'} "
+                        f"Q{frac_bits}/i{int_bits}",
+            "ms": round(ms, 5), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms)}
+
+
+WORKLOADS = {
+    "rms_norm": lambda s, w: wl_rms_norm(s, w, 32, 16),
+    "rms_norm_q32i64": lambda s, w: wl_rms_norm(s, w, 64, 32),
+    "log_softmax": lambda s, w: wl_log_softmax(s, w, 32, 16),
+    "log_softmax_f32out_q32i64": lambda s, w: wl_log_softmax(s, w, 64, 32, fp32_out=True),
+}
+HEADLINE_ORDER = ["gemm_lm_head", "decode_attn", "rms_norm"]
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the numpy oracle on a bounded sample of the headline workload
+
+
+def cpu_baseline(headline: str, budget_s: float) -> dict:
+    import numpy as np
+
+    from oracle import rows as OR
+
+    threads = 1  # numpy elementwise arithmetic runs on one core
+    if headline.startswith("rms_norm"):
+        H = 4096
+        rows = 64
+        rng = np.random.default_rng(0)
+        x = (rng.standard_normal((rows, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        r = (rng.standard_normal((rows, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        w = np.full(H, 0x3F80, np.uint16)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            OR.rms_norm(x, w, 1e-6, "bf16", 32, 16, residual=r)
+            reps += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        dt = (time.perf_counter() - t0) / reps
+        gbs = 4 * rows * H * 2 / dt / 1e9
+        return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"oracle.rows.rms_norm bf16 [{rows},{H}] + residual, Q16/i32, "
+                          f"{reps} reps in {budget_s:.0f}s"}
+    raise ValueError(headline)
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workloads", default="all")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(requested --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import fxpr_vllm  # noqa: F401
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+
+    names = list(WORKLOADS) if args.workloads == "all" else args.workloads.split(",")
+    results = {}
+    for name in names:
+        log(f"workload {name} ...")
+        results[name] = WORKLOADS[name](args.steps, args.warmup)
+        log(f"  {json.dumps(results[name])}")
+
+    headline = next((h for h in HEADLINE_ORDER if h in results), names[0])
+    head = results[headline]
+    rf = head["roofline"]
+    value = rf["achieved"]
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": rf["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 in, int32 fixed-point accumulate",
+        "data": "synthetic (seeded torch CPU generator, copied to HBM)",
+        "config": {"workload": head["workload"], "headline": headline},
+        "roofline": rf,
+        "extra": {k: v for k, v in results.items() if k != headline},
+        "host": {"cpu_count": os.cpu_count(), "cpu_model": cpu_model(),
+                 "torch_threads": torch.get_num_threads(),
+                 "gpu": torch.cuda.get_device_name(0)},
+    }
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(headline, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

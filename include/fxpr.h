@@ -111,6 +111,37 @@ int fxpr_log_softmax(const void* x, int x_dtype, void* y, int y_dtype,
                      int64_t rows, int64_t cols, int int_bits, int frac_bits,
                      void* stream);
 
+/*
+ * Fixed-point GEMM, C[M,N] = IO(fl32(acc) * 2^-frac_bits (+ bias)) with
+ * acc = wrapping int_bits sum over K-tiles t (128 wide for bf16/f16, 64 for
+ * f32; zero-padded tail) of RNE_sat(fp32 dot(A[m, t], B[t, n]) * 2^f).
+ * io_dtype (bf16 / f16 / f32) is the type of A, B and C; bias is NULL or N
+ * fp32 values. Strides are in elements: A must have stride_ak == 1; B must
+ * have stride_bk == 1 (column-major, e.g. a transposed [N,K] weight) or
+ * stride_bn == 1 (row-major [K,N]). split_k: 0 = automatic, >= 1 = that many
+ * K-splits (clamped to the K-tile count); split counts never change bits.
+ * When the resolved split count is > 1 a workspace of
+ * fxpr_gemm_workspace_bytes() bytes is required (caller-owned, no zeroing).
+ * Replaces gemm_fxp_run + _gemm_kernel / _gemm_splitk_kernel
+ * (fxpr_vllm/_triton/gemm.py:612-763, 123-204, 209-325).
+ */
+int fxpr_gemm(const void* a, const void* b, const float* bias, void* c,
+              int io_dtype, int64_t m, int64_t n, int64_t k,
+              int64_t stride_am, int64_t stride_ak, int64_t stride_bk,
+              int64_t stride_bn, int64_t stride_cm, int64_t stride_cn,
+              int int_bits, int frac_bits, int split_k, void* workspace,
+              int64_t workspace_bytes, void* stream);
+
+/* Split count fxpr_gemm will use for this shape and request.
+ * Host-side policy of the reference: _resolve_split_k (gemm.py:385-412). */
+int fxpr_gemm_splits(int64_t m, int64_t n, int64_t k, int io_dtype,
+                     int split_k);
+
+/* Workspace bytes fxpr_gemm needs for this shape and request (0 = none).
+ * Replaces the persistent scratch of gemm.py:61-107. */
+int64_t fxpr_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k,
+                                  int io_dtype, int int_bits, int split_k);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in fxpr.h but not exported"
     # every declared symbol is also bound with a signature on the Python side
-    bound = set(_hip.SIGNATURES) | {"fxpr_error_string", "fxpr_abi_version"}
+    bound = set(_hip.SIGNATURES) | set(_hip.RESTYPES) | {"fxpr_error_string", "fxpr_abi_version"}
     assert set(names) <= bound, set(names) - bound
 
 

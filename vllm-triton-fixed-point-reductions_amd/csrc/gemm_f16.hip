@@ -1,0 +1,16 @@
+// Fixed-point GEMM kernels instantiated for f16 inputs (see gemm_impl.h).
+#include "gemm_impl.h"
+
+namespace fxpr {
+namespace gemm {
+
+int run_gemm_f16(const GemmArgs& a, int bits, bool b_ncontig, bool vec, int splits, hipStream_t st) {
+  switch (bits) {
+    case 16: return run_gemm<FXPR_DTYPE_F16, 16>(a, b_ncontig, vec, splits, st);
+    case 32: return run_gemm<FXPR_DTYPE_F16, 32>(a, b_ncontig, vec, splits, st);
+    default: return run_gemm<FXPR_DTYPE_F16, 64>(a, b_ncontig, vec, splits, st);
+  }
+}
+
+}  // namespace gemm
+}  // namespace fxpr

@@ -1,0 +1,447 @@
+// Fixed-point GEMM on MFMA (gfx950).
+//
+//   C[m, n] = IO( fl32(acc) * 2^-f (+ fl32(bias[n])) ),
+//   acc     = sum over K-tiles t (wrapping b-bit) of RNE_sat_b(P_t[m, n] * 2^f),
+//   P_t     = fp32 dot of A[m, tile t] and B[tile t, n] (K tail zero-padded).
+//
+// Replaces _gemm_kernel / _gemm_splitk_kernel (fxpr_vllm/_triton/gemm.py:
+// 123-204, 209-325). The K-tile width (128 for bf16/f16, 64 for fp32) is the
+// determinism unit of the reference (gemm.py:18-31) and is kept. Every output
+// element's P_t is produced by the same fixed chain of MFMA instructions
+// (16x16x32 bf16/f16, 16x16x4 f32) in increasing k order, whatever the tile
+// configuration, M, N or split count, so results are bitwise invariant to
+// all of them. Split-K writes per-split integer partials to a workspace and
+// a second kernel sums them; integer addition makes the order irrelevant and
+// no atomics or counters are needed (graph-capturable, nothing to re-zero).
+
+#pragma once
+
+#include "fxp_device.h"
+#include "fxpr_internal.h"
+
+namespace fxpr {
+namespace gemm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;  // 4 waves per workgroup
+
+// Per-dtype MFMA traits: KI = k per instruction, BKQ = quantisation K-tile,
+// BKS = k per LDS stage, CHUNK = elements per 16-byte vector.
+template <int DT> struct Mma;
+template <> struct Mma<FXPR_DTYPE_BF16> {
+  using T = uint16_t;
+  using Frag = uint4;
+  static constexpr int KI = 32, BKQ = 128, BKS = 64, CHUNK = 8;
+  static __device__ __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mma<FXPR_DTYPE_F16> {
+  using T = uint16_t;
+  using Frag = uint4;
+  static constexpr int KI = 32, BKQ = 128, BKS = 64, CHUNK = 8;
+  static __device__ __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mma<FXPR_DTYPE_F32> {
+  using T = float;
+  using Frag = float;
+  static constexpr int KI = 4, BKQ = 64, BKS = 32, CHUNK = 4;
+  static __device__ __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+template <int BM_, int BN_, int WM_, int WN_> struct Tile {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int WAVES_N = BN / WN;
+  static constexpr int MB = WM / 16, NB = WN / 16;
+  static_assert((BM / WM) * (BN / WN) == kThreads / 64, "4 waves per workgroup");
+};
+
+struct GemmArgs {
+  const void* a;
+  const void* b;
+  const float* bias;  // fp32 copy of the bias (exact for bf16 / f16 biases) or null
+  void* c;
+  void* ws;          // split-K partials [splits][M][N] (int32 or int64)
+  int64_t M, N, K;
+  int64_t lda;       // A row stride (A is K-contiguous)
+  int64_t ldb;       // B: stride between n columns (K-contiguous) or k rows (N-contiguous)
+  int64_t scm, scn;  // C strides
+  float scale, inv_scale;
+  int ktiles, tiles_per_split, tiles_m, tiles_n;
+};
+
+template <int BITS> struct Acc { using T = int32_t; };
+template <> struct Acc<64> { using T = int64_t; };
+
+template <int BITS> __device__ __forceinline__ typename Acc<BITS>::T wrap_add(typename Acc<BITS>::T a, int64_t q) {
+  if constexpr (BITS == 64) return static_cast<int64_t>(static_cast<uint64_t>(a) + static_cast<uint64_t>(q));
+  else return static_cast<int32_t>(static_cast<uint32_t>(a) + static_cast<uint32_t>(q));
+}
+
+// fl32 of the b-bit two's-complement value held in the accumulator.
+template <int BITS> __device__ __forceinline__ float acc_to_f32(typename Acc<BITS>::T v, float inv) {
+  if constexpr (BITS == 16) return fixed_to_f32(static_cast<int32_t>(static_cast<int16_t>(v)), inv);
+  else return fixed_to_f32(v, inv);
+}
+
+// 16 bytes of CHUNK consecutive elements at p (unit stride), the first
+// `valid` of them real and the rest zero.
+template <bool VEC, typename T>
+__device__ __forceinline__ uint4 load_chunk(const T* p, int valid) {
+  constexpr int CH = 16 / sizeof(T);
+  if (VEC && valid == CH) return *reinterpret_cast<const uint4*>(p);
+  union {
+    uint4 v;
+    T e[CH];
+  } u;
+  u.v = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < CH; ++j)
+    if (j < valid) u.e[j] = p[j];
+  return u.v;
+}
+
+// Workgroup tile -> (tm, tn). Hardware hands consecutive workgroup ids to the
+// 8 XCDs round-robin; remap so each XCD gets one contiguous run of logical
+// tiles (L2 reuse), then group GROUP_M row tiles per column sweep.
+__device__ __forceinline__ void tile_coords(int bid, int nblk, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int q = nblk >> 3, r = nblk & 7, x = bid & 7, i = bid >> 3;
+  const int logical = x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+  constexpr int GROUP_M = 8;
+  const int per_group = GROUP_M * tiles_n;
+  const int g = logical / per_group;
+  const int first_m = g * GROUP_M;
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  tm = first_m + (logical % per_group) % gsize;
+  tn = (logical % per_group) / gsize;
+}
+
+template <int DT, int BITS, class TL, bool B_NCONTIG, bool VEC, bool SPLIT>
+__global__ __launch_bounds__(kThreads) void gemm_fxp_kernel(GemmArgs args) {
+  using M_ = Mma<DT>;
+  using T = typename M_::T;
+  using Frag = typename M_::Frag;
+  using AccT = typename Acc<BITS>::T;
+  constexpr int BM = TL::BM, BN = TL::BN, MB = TL::MB, NB = TL::NB;
+  constexpr int BKS = M_::BKS, KI = M_::KI, CH = M_::CHUNK;
+  constexpr int LDS_K = BKS + CH;  // row pitch in elements (+16 B pad vs bank conflicts)
+  constexpr int SPT = M_::BKQ / BKS;  // LDS stages per quantisation tile
+  constexpr int CPR = BKS / CH;       // 16-byte chunks per row of a stage
+  constexpr int NA = (BM * CPR + kThreads - 1) / kThreads;
+  constexpr int NBC = (BN * CPR + kThreads - 1) / kThreads;
+
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* As = reinterpret_cast<T*>(smem_raw);                 // [2][BM][LDS_K]
+  T* Bs = As + 2 * BM * LDS_K;                            // [2][BN][LDS_K]
+
+  const T* A = static_cast<const T*>(args.a);
+  const T* B = static_cast<const T*>(args.b);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / TL::WAVES_N, wn = wave % TL::WAVES_N;
+  int tm, tn;
+  tile_coords(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, tm, tn);
+  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+  const int split = blockIdx.y;
+  const int kt_begin = split * args.tiles_per_split;
+  const int kt_end = min(args.ktiles, kt_begin + args.tiles_per_split);
+  const int nstages = max(0, kt_end - kt_begin) * SPT;
+  const int64_t k_base = int64_t(kt_begin) * M_::BKQ;
+
+  uint4 ra[NA], rb[NBC];
+
+  auto gload = [&](int s) {
+    const int64_t k0 = k_base + int64_t(s) * BKS;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < BM * CPR) {
+        const int row = c / CPR, kc = (c % CPR) * CH;
+        const int64_t m = m0 + row, k = k0 + kc;
+        const int valid = (m < args.M && k < args.K) ? int(min<int64_t>(CH, args.K - k)) : 0;
+        ra[i] = load_chunk<VEC>(A + (valid ? m * args.lda + k : 0), valid);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NBC; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < BN * CPR) {
+        if constexpr (!B_NCONTIG) {  // B column n has unit k stride
+          const int col = c / CPR, kc = (c % CPR) * CH;
+          const int64_t n = n0 + col, k = k0 + kc;
+          const int valid = (n < args.N && k < args.K) ? int(min<int64_t>(CH, args.K - k)) : 0;
+          rb[i] = load_chunk<VEC>(B + (valid ? n * args.ldb + k : 0), valid);
+        } else {  // B row k has unit n stride
+          constexpr int CPRN = BN / CH;
+          const int krow = c / CPRN, nc = (c % CPRN) * CH;
+          const int64_t k = k0 + krow, n = n0 + nc;
+          const int valid = (k < args.K && n < args.N) ? int(min<int64_t>(CH, args.N - n)) : 0;
+          rb[i] = load_chunk<VEC>(B + (valid ? k * args.ldb + n : 0), valid);
+        }
+      }
+    }
+  };
+
+  auto lstore = [&](int buf) {
+    T* as = As + buf * BM * LDS_K;
+    T* bs = Bs + buf * BN * LDS_K;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < BM * CPR) *reinterpret_cast<uint4*>(as + (c / CPR) * LDS_K + (c % CPR) * CH) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NBC; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < BN * CPR) {
+        if constexpr (!B_NCONTIG) {
+          *reinterpret_cast<uint4*>(bs + (c / CPR) * LDS_K + (c % CPR) * CH) = rb[i];
+        } else {
+          constexpr int CPRN = BN / CH;
+          const int krow = c / CPRN, nc = (c % CPRN) * CH;
+          union {
+            uint4 v;
+            T e[CH];
+          } u;
+          u.v = rb[i];
+#pragma unroll
+          for (int j = 0; j < CH; ++j) bs[(nc + j) * LDS_K + krow] = u.e[j];
+        }
+      }
+    }
+  };
+
+  f32x4 P[MB][NB];
+  AccT I[MB][NB][4];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      P[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) I[i][j][r] = 0;
+    }
+
+  const int frag_row = lane & 15, frag_k = (lane >> 4) * (KI / 4);
+
+  if (nstages > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int s = 0; s < nstages; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nstages) gload(s + 1);
+    const T* as = As + buf * BM * LDS_K + (wm * TL::WM + frag_row) * LDS_K + frag_k;
+    const T* bs = Bs + buf * BN * LDS_K + (wn * TL::WN + frag_row) * LDS_K + frag_k;
+#pragma unroll
+    for (int kk = 0; kk < BKS; kk += KI) {
+      Frag fa[MB], fb[NB];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) fa[i] = *reinterpret_cast<const Frag*>(as + i * 16 * LDS_K + kk);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) fb[j] = *reinterpret_cast<const Frag*>(bs + j * 16 * LDS_K + kk);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) P[i][j] = M_::mma(fa[i], fb[j], P[i][j]);
+    }
+    if (s % SPT == SPT - 1) {  // a quantisation tile is complete
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            I[i][j][r] = wrap_add<BITS>(I[i][j][r], quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
+          P[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    if (s + 1 < nstages) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue. Lane holds rows 4*(lane/16)+r of each 16x16 block, column lane%16.
+  const int64_t row_base = m0 + wm * TL::WM + (lane >> 4) * 4;
+  const int64_t col_base = n0 + wn * TL::WN + (lane & 15);
+  if constexpr (SPLIT) {
+    AccT* ws = static_cast<AccT*>(args.ws) + int64_t(split) * args.M * args.N;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int64_t n = col_base + j * 16;
+        if (n >= args.N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = row_base + i * 16 + r;
+          if (m < args.M) ws[m * args.N + n] = I[i][j][r];
+        }
+      }
+  } else {
+    T* C = static_cast<T*>(args.c);
+    const float* bias = args.bias;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int64_t n = col_base + j * 16;
+      if (n >= args.N) continue;
+      const float bv = bias ? bias[n] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = row_base + i * 16 + r;
+          if (m >= args.M) continue;
+          float v = acc_to_f32<BITS>(I[i][j][r], args.inv_scale);
+          if (bias) v = __fadd_rn(v, bv);
+          C[m * args.scm + n * args.scn] = Io<DT>::store(v);
+        }
+    }
+  }
+}
+
+// Sum the per-split integer partials (wrapping b-bit) and apply the epilogue.
+template <int DT, int BITS>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, int splits) {
+  using T = typename Io<DT>::T;
+  using AccT = typename Acc<BITS>::T;
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t MN = args.M * args.N;
+  if (idx >= MN) return;
+  const AccT* ws = static_cast<const AccT*>(args.ws);
+  AccT acc = 0;
+  for (int s = 0; s < splits; ++s) acc = wrap_add<BITS>(acc, ws[int64_t(s) * MN + idx]);
+  const int64_t m = idx / args.N, n = idx % args.N;
+  float v = acc_to_f32<BITS>(acc, args.inv_scale);
+  if (args.bias) v = __fadd_rn(v, args.bias[n]);
+  static_cast<T*>(args.c)[m * args.scm + n * args.scn] = Io<DT>::store(v);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+template <int DT, class TL> constexpr size_t lds_bytes() {
+  return size_t(2) * (TL::BM + TL::BN) * (Mma<DT>::BKS + Mma<DT>::CHUNK) * sizeof(typename Mma<DT>::T);
+}
+
+template <int DT, int BITS, class TL, bool BN_, bool VEC, bool SPLIT>
+int launch_tile(const GemmArgs& a, int splits, hipStream_t st) {
+  auto kern = gemm_fxp_kernel<DT, BITS, TL, BN_, VEC, SPLIT>;
+  constexpr size_t lds = lds_bytes<DT, TL>();
+  static bool attr_done = false;  // benign race: the attribute is idempotent
+  if (!attr_done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (e != hipSuccess) return int(e);
+    attr_done = true;
+  }
+  dim3 grid(unsigned(a.tiles_m * a.tiles_n), unsigned(splits));
+  kern<<<grid, kThreads, lds, st>>>(a);
+  return launch_status();
+}
+
+template <int DT, int BITS, class TL, bool BNC, bool VEC>
+int launch_cfg(GemmArgs a, int splits, hipStream_t st) {
+  a.tiles_m = int(cdiv(a.M, TL::BM));
+  a.tiles_n = int(cdiv(a.N, TL::BN));
+  if (splits > 1) return launch_tile<DT, BITS, TL, BNC, VEC, true>(a, splits, st);
+  return launch_tile<DT, BITS, TL, BNC, VEC, false>(a, splits, st);
+}
+
+// Tile configuration by M. Only speed depends on it: every config issues the
+// same MFMA chain per output element.
+enum class TileId { M16, M32, M64, Big };
+inline TileId pick_tile(int64_t M) {
+  if (M <= 16) return TileId::M16;
+  if (M <= 32) return TileId::M32;
+  if (M <= 64) return TileId::M64;
+  return TileId::Big;
+}
+using T16 = Tile<16, 256, 16, 64>;
+using T32 = Tile<32, 256, 32, 64>;
+using T64 = Tile<64, 256, 64, 64>;
+using TBig = Tile<128, 128, 64, 64>;
+
+inline void tile_dims(TileId t, int& bm, int& bn) {
+  switch (t) {
+    case TileId::M16: bm = T16::BM; bn = T16::BN; break;
+    case TileId::M32: bm = T32::BM; bn = T32::BN; break;
+    case TileId::M64: bm = T64::BM; bn = T64::BN; break;
+    default: bm = TBig::BM; bn = TBig::BN; break;
+  }
+}
+
+// Instantiation matrix: the vectorised K-contiguous-B path (weights as
+// stored by the vLLM glue) gets every tile; the N-contiguous-B path gets a
+// skinny and a square tile; misaligned / ragged operands (scalar loads) use
+// the square tile only. Tile choice never changes bits.
+template <int DT, int BITS>
+int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
+  const TileId t = pick_tile(a.M);
+  if (vec && !b_ncontig) {
+    switch (t) {
+      case TileId::M16: return launch_cfg<DT, BITS, T16, false, true>(a, splits, st);
+      case TileId::M32: return launch_cfg<DT, BITS, T32, false, true>(a, splits, st);
+      case TileId::M64: return launch_cfg<DT, BITS, T64, false, true>(a, splits, st);
+      default: return launch_cfg<DT, BITS, TBig, false, true>(a, splits, st);
+    }
+  }
+  if (vec) {
+    if (t == TileId::M16) return launch_cfg<DT, BITS, T16, true, true>(a, splits, st);
+    return launch_cfg<DT, BITS, TBig, true, true>(a, splits, st);
+  }
+  if (b_ncontig) return launch_cfg<DT, BITS, TBig, true, false>(a, splits, st);
+  return launch_cfg<DT, BITS, TBig, false, false>(a, splits, st);
+}
+
+template <int DT, int BITS>
+int run_gemm(GemmArgs a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
+  int rc = dispatch_tile<DT, BITS>(a, b_ncontig, vec, splits, st);
+  if (rc != FXPR_OK || splits <= 1) return rc;
+  const int64_t mn = a.M * a.N;
+  gemm_splitk_reduce_kernel<DT, BITS><<<dim3(unsigned(cdiv(mn, 256))), 256, 0, st>>>(a, splits);
+  return launch_status();
+}
+
+inline int ktile_for(int io_dtype) { return io_dtype == FXPR_DTYPE_F32 ? 64 : 128; }
+
+// Split count: explicit request wins (clamped to the K-tile count); otherwise
+// split only when the output tiles cannot fill the 256 CUs about twice.
+inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int requested) {
+  const int ktiles = int(cdiv(K, ktile_for(io_dtype)));
+  if (ktiles <= 1) return 1;
+  int s;
+  if (requested >= 1) {
+    s = requested;
+  } else {
+    int bm, bn;
+    tile_dims(pick_tile(M), bm, bn);
+    const int64_t tiles = cdiv(M, bm) * cdiv(N, bn);
+    if (tiles >= 256) return 1;
+    s = int(512 / tiles);
+    if (s > 16) s = 16;
+  }
+  if (s > ktiles) s = ktiles;
+  return s < 1 ? 1 : s;
+}
+
+inline int64_t ws_bytes_for(int64_t M, int64_t N, int int_bits, int splits) {
+  return splits > 1 ? int64_t(splits) * M * N * (int_bits == 64 ? 8 : 4) : 0;
+}
+
+
+// Per-dtype entry (one translation unit each, built in parallel).
+int run_gemm_bf16(const GemmArgs& a, int bits, bool b_ncontig, bool vec, int splits, hipStream_t st);
+int run_gemm_f16(const GemmArgs& a, int bits, bool b_ncontig, bool vec, int splits, hipStream_t st);
+int run_gemm_f32(const GemmArgs& a, int bits, bool b_ncontig, bool vec, int splits, hipStream_t st);
+
+}  // namespace gemm
+}  // namespace fxpr

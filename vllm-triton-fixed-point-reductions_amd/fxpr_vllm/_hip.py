@@ -36,7 +36,12 @@ SIGNATURES: dict[str, list] = {
     "fxpr_fixed_row_sum": [_P, _I, _P, _I, _L, _L, _P],
     "fxpr_rms_norm": [_P, _P, _P, _P, _I, _L, _L, _F, _I, _I, _P],
     "fxpr_log_softmax": [_P, _I, _P, _I, _L, _L, _I, _I, _P],
+    "fxpr_gemm": [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _P],
+    "fxpr_gemm_splits": [_L, _L, _L, _I, _I],
 }
+
+# entry points that return something other than an int status
+RESTYPES = {"fxpr_gemm_workspace_bytes": ([_L, _L, _L, _I, _I, _I], _L)}
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()
@@ -64,6 +69,10 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
                 fn.restype = _I
+            for name, (argtypes, restype) in RESTYPES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                fn.restype = restype
             _lib = lib
     return _lib
 

@@ -14,6 +14,7 @@ from __future__ import annotations
 import torch
 
 from ._kernels import casts as _casts
+from ._kernels import gemm as _gemm
 from ._kernels import rows as _rows
 
 _lib = torch.library.Library("fxpr", "DEF")
@@ -76,6 +77,13 @@ def _rms_norm_fxp_residual_cuda(x: torch.Tensor, residual: torch.Tensor,
     return _rows.rms_norm_fxp_residual_run(x, residual, weight, float(eps))
 
 
+def _gemm_fxp_cuda(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None,
+                   fxp_int_bits: int, fxp_frac_bits: int):
+    _check_int_bits(fxp_int_bits)
+    _check_frac_bits(fxp_frac_bits)
+    return _gemm.gemm_fxp_run(a, b, bias, int(fxp_int_bits), int(fxp_frac_bits))
+
+
 def _fixed_row_sum_cuda(q: torch.Tensor, int_bits: int):
     _check_int_bits(int_bits)
     return _rows.fixed_row_sum_run(q, int(int_bits))
@@ -93,5 +101,6 @@ _lib.impl("float_to_fixed", _float_to_fixed_cuda, "CUDA")
 _lib.impl("fixed_to_float", _fixed_to_float_cuda, "CUDA")
 _lib.impl("rms_norm_fxp", _rms_norm_fxp_cuda, "CUDA")
 _lib.impl("rms_norm_fxp_residual", _rms_norm_fxp_residual_cuda, "CUDA")
+_lib.impl("gemm_fxp", _gemm_fxp_cuda, "CUDA")
 _lib.impl("fixed_row_sum", _fixed_row_sum_cuda, "CUDA")
 _lib.impl("log_softmax_fxp", _log_softmax_fxp_cuda, "CUDA")
