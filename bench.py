@@ -144,7 +144,69 @@ def wl_log_softmax(steps, warmup, int_bits=32, frac_bits=16, fp32_out=False, R=2
             "ms": round(ms, 5), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms)}
 
 
+_WEIGHTS: dict = {}
+
+
+def _weight(N, K, dtype, std, seed):
+    """[N, K] row-major weight (vLLM's layout), seeded on the CPU, cached."""
+    import torch
+
+    key = (N, K, dtype, std, seed)
+    if key not in _WEIGHTS:
+        g = torch.Generator("cpu").manual_seed(seed)
+        w = torch.empty(N, K, dtype=dtype)
+        step = 8192
+        for i in range(0, N, step):  # bounded host memory
+            w[i:i + step] = (torch.randn(min(step, N - i), K, generator=g) * std).to(dtype)
+        _WEIGHTS.clear()
+        _WEIGHTS[key] = w.to("cuda")
+    return _WEIGHTS[key]
+
+
+def wl_gemm(steps, warmup, M, N=128256, K=4096, dtype_name="bf16", int_bits=32, frac_bits=16,
+            split_k=0):
+    """lm_head / linear GEMM. B = W^T with W [N, K] row-major: the K-contiguous
+    layout the fixed-point linear method keeps (no transposed copy)."""
+    import torch
+
+    from fxpr_vllm._kernels import gemm as KG
+
+    dtype = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype_name]
+    esz = torch.tensor([], dtype=dtype).element_size()
+    w = _weight(N, K, dtype, 0.02, seed=1)
+    g = torch.Generator("cpu").manual_seed(2)
+    b_bytes = N * K * esz
+    a = torch.randn(M, K, generator=g).to(dtype).to("cuda")
+    sets = [(a, w.t())]
+    if b_bytes * 2 < 2 * MALL_BYTES:  # weights that fit in the MALL: rotate copies
+        sets += [(a, w.clone().t()) for _ in range(copies_for(b_bytes) - 1)]
+
+    def fn(aa, bb):
+        return KG.gemm_fxp_run(aa, bb, None, int_bits, frac_bits, split_k=split_k)
+
+    ms = time_op(fn, sets, steps, warmup)
+    flops = 2.0 * M * N * K
+    nbytes = esz * (M * K + K * N + M * N)
+    peak = FP32_PEAK_TFLOPS if dtype == torch.float32 else BF16_PEAK_TFLOPS
+    res = {"workload": f"gemm_fxp {dtype_name} A[{M},{K}] x B[{K},{N}] (B K-contiguous) "
+                       f"Q{frac_bits}/i{int_bits}",
+           "ms": round(ms, 5), "flops": flops, "bytes": nbytes,
+           "splits": KG.resolve_split_k(M, N, K, dtype, split_k),
+           "mfma": mfma_roofline(flops, ms, peak), "hbm": hbm_roofline(nbytes, ms)}
+    # the bounding roofline: HBM for skinny M, MFMA from the ridge point on
+    res["roofline"] = res["mfma"] if flops / nbytes > peak * 1e12 / (HBM_PEAK_GBS * 1e9) else res["hbm"]
+    return res
+
+
 WORKLOADS = {
+    "gemm_lm_head": lambda s, w: wl_gemm(s, w, 8192),
+    "gemm_lm_head_m2048": lambda s, w: wl_gemm(s, w, 2048),
+    "gemm_lm_head_m256": lambda s, w: wl_gemm(s, w, 256),
+    "gemm_lm_head_m32": lambda s, w: wl_gemm(s, w, 32),
+    "gemm_lm_head_m1": lambda s, w: wl_gemm(s, w, 1),
+    "gemm_lm_head_m8192_i64": lambda s, w: wl_gemm(s, w, 8192, int_bits=64),
+    "gemm_f16_14336_m8192": lambda s, w: wl_gemm(s, w, 8192, N=14336, dtype_name="f16"),
+    "gemm_f32_14336_m8192": lambda s, w: wl_gemm(max(3, s // 4), 1, 8192, N=14336, dtype_name="f32"),
     "rms_norm": lambda s, w: wl_rms_norm(s, w, 32, 16),
     "rms_norm_q32i64": lambda s, w: wl_rms_norm(s, w, 64, 32),
     "log_softmax": lambda s, w: wl_log_softmax(s, w, 32, 16),
@@ -163,6 +225,30 @@ def cpu_baseline(headline: str, budget_s: float) -> dict:
     from oracle import rows as OR
 
     threads = 1  # numpy elementwise arithmetic runs on one core
+    if headline.startswith("gemm"):
+        from oracle import gemm as OG
+
+        try:
+            from threadpoolctl import threadpool_info
+
+            threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+        except Exception:  # noqa: BLE001
+            threads = os.cpu_count() or 1
+        M, K, Nn = 64, 4096, 2048
+        rng = np.random.default_rng(0)
+        a = (rng.standard_normal((M, K)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        b = ((rng.standard_normal((K, Nn)) * 0.02).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            OG.gemm(a, b, None, "bf16", 32, 16)
+            reps += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(2.0 * M * K * Nn / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+                "kind": "port",
+                "sample": f"oracle.gemm.gemm bf16 A[{M},{K}] x B[{K},{Nn}] Q16/i32 (numpy, BLAS "
+                          f"float64 tile dots), {reps} reps in {budget_s:.0f}s"}
     if headline.startswith("rms_norm"):
         H = 4096
         rows = 64
@@ -215,6 +301,7 @@ def main() -> None:
         log(f"  {json.dumps(results[name])}")
 
     headline = next((h for h in HEADLINE_ORDER if h in results), names[0])
+    _WEIGHTS.clear()
     head = results[headline]
     rf = head["roofline"]
     value = rf["achieved"]
@@ -229,7 +316,8 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 in, int32 fixed-point accumulate",
+        "dtype": "bf16 MFMA, int32 fixed-point accumulate" if headline.startswith("gemm")
+                 else "bf16 in, int32 fixed-point accumulate",
         "data": "synthetic (seeded torch CPU generator, copied to HBM)",
         "config": {"workload": head["workload"], "headline": headline},
         "roofline": rf,

@@ -24,7 +24,7 @@ extern "C" int fxpr_gemm(const void* a, const void* b, const float* bias, void* 
   if (!valid_int_bits(int_bits) || frac_bits < 0 || frac_bits > 63) return FXPR_E_BITS;
   if (m < 0 || n < 0 || k < 0 || split_k < 0) return FXPR_E_SHAPE;
   if (m == 0 || n == 0) return FXPR_OK;
-  if (!a || !b || !c) return FXPR_E_ARG;
+  if (!c || (k > 0 && (!a || !b))) return FXPR_E_ARG;  // K = 0: C = bias (or 0)
   if (io_dtype != FXPR_DTYPE_BF16 && io_dtype != FXPR_DTYPE_F16 && io_dtype != FXPR_DTYPE_F32)
     return FXPR_E_DTYPE;
   if (stride_ak != 1 && k > 1) return FXPR_E_ARG;  // A must be K-contiguous

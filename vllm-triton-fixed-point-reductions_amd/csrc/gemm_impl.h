@@ -133,15 +133,16 @@ __global__ __launch_bounds__(kThreads) void gemm_fxp_kernel(GemmArgs args) {
   using AccT = typename Acc<BITS>::T;
   constexpr int BM = TL::BM, BN = TL::BN, MB = TL::MB, NB = TL::NB;
   constexpr int BKS = M_::BKS, KI = M_::KI, CH = M_::CHUNK;
-  constexpr int LDS_K = BKS + CH;  // row pitch in elements (+16 B pad vs bank conflicts)
+  constexpr int LDS_K = BKS + CH;     // row pitch in elements (+16 B pad vs bank conflicts)
   constexpr int SPT = M_::BKQ / BKS;  // LDS stages per quantisation tile
   constexpr int CPR = BKS / CH;       // 16-byte chunks per row of a stage
+  constexpr int CPRN = BN / CH;       // chunks per k-row of B when N-contiguous
   constexpr int NA = (BM * CPR + kThreads - 1) / kThreads;
   constexpr int NBC = (BN * CPR + kThreads - 1) / kThreads;
 
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* As = reinterpret_cast<T*>(smem_raw);                 // [2][BM][LDS_K]
-  T* Bs = As + 2 * BM * LDS_K;                            // [2][BN][LDS_K]
+  T* As = reinterpret_cast<T*>(smem_raw);  // [2][BM][LDS_K]
+  T* Bs = As + 2 * BM * LDS_K;             // [2][BN][LDS_K]
 
   const T* A = static_cast<const T*>(args.a);
   const T* B = static_cast<const T*>(args.b);
@@ -153,39 +154,71 @@ __global__ __launch_bounds__(kThreads) void gemm_fxp_kernel(GemmArgs args) {
   const int split = blockIdx.y;
   const int kt_begin = split * args.tiles_per_split;
   const int kt_end = min(args.ktiles, kt_begin + args.tiles_per_split);
-  const int nstages = max(0, kt_end - kt_begin) * SPT;
+  const int ntiles = max(0, kt_end - kt_begin);
+  const int nstages = ntiles * SPT;
   const int64_t k_base = int64_t(kt_begin) * M_::BKQ;
+
+  // Per-thread chunk pointers at k = k_base. Rows (columns) past M (N) are
+  // clamped to the last valid one: they only feed outputs that are never
+  // stored, since an MFMA output row (column) depends on its own A row (B
+  // column) only.
+  const T* pa[NA];
+  const T* pb[NBC];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int c = min(tid + i * kThreads, BM * CPR - 1);
+    const int64_t m = min<int64_t>(m0 + c / CPR, args.M - 1);
+    pa[i] = A + m * args.lda + k_base + (c % CPR) * CH;
+  }
+#pragma unroll
+  for (int i = 0; i < NBC; ++i) {
+    const int c = min(tid + i * kThreads, BN * CPR - 1);
+    if constexpr (!B_NCONTIG) {
+      const int64_t n = min<int64_t>(n0 + c / CPR, args.N - 1);
+      pb[i] = B + n * args.ldb + k_base + (c % CPR) * CH;
+    } else {
+      const int64_t n = min<int64_t>(n0 + (c % CPRN) * CH, args.N - CH);
+      pb[i] = B + (k_base + c / CPRN) * args.ldb + (n < 0 ? 0 : n);
+    }
+  }
 
   uint4 ra[NA], rb[NBC];
 
+  // Stage s covers k in [k_base + s*BKS, k_base + (s+1)*BKS).
   auto gload = [&](int s) {
     const int64_t k0 = k_base + int64_t(s) * BKS;
+    if (VEC && k0 + BKS <= args.K) {  // full stage: plain 16-byte loads
+#pragma unroll
+      for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const uint4*>(pa[i] + int64_t(s) * BKS);
+#pragma unroll
+      for (int i = 0; i < NBC; ++i) {
+        const int64_t off = B_NCONTIG ? int64_t(s) * BKS * args.ldb : int64_t(s) * BKS;
+        rb[i] = *reinterpret_cast<const uint4*>(pb[i] + off);
+      }
+      return;
+    }
+    // K tail (or unaligned operands): masked element loads, zero fill
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int c = tid + i * kThreads;
-      if (c < BM * CPR) {
-        const int row = c / CPR, kc = (c % CPR) * CH;
-        const int64_t m = m0 + row, k = k0 + kc;
-        const int valid = (m < args.M && k < args.K) ? int(min<int64_t>(CH, args.K - k)) : 0;
-        ra[i] = load_chunk<VEC>(A + (valid ? m * args.lda + k : 0), valid);
-      }
+      const int row = c / CPR, kc = (c % CPR) * CH;
+      const int64_t m = m0 + row, k = k0 + kc;
+      const int valid = (c < BM * CPR && m < args.M && k < args.K) ? int(min<int64_t>(CH, args.K - k)) : 0;
+      ra[i] = load_chunk<false>(A + (valid ? m * args.lda + k : 0), valid);
     }
 #pragma unroll
     for (int i = 0; i < NBC; ++i) {
       const int c = tid + i * kThreads;
-      if (c < BN * CPR) {
-        if constexpr (!B_NCONTIG) {  // B column n has unit k stride
-          const int col = c / CPR, kc = (c % CPR) * CH;
-          const int64_t n = n0 + col, k = k0 + kc;
-          const int valid = (n < args.N && k < args.K) ? int(min<int64_t>(CH, args.K - k)) : 0;
-          rb[i] = load_chunk<VEC>(B + (valid ? n * args.ldb + k : 0), valid);
-        } else {  // B row k has unit n stride
-          constexpr int CPRN = BN / CH;
-          const int krow = c / CPRN, nc = (c % CPRN) * CH;
-          const int64_t k = k0 + krow, n = n0 + nc;
-          const int valid = (k < args.K && n < args.N) ? int(min<int64_t>(CH, args.N - n)) : 0;
-          rb[i] = load_chunk<VEC>(B + (valid ? k * args.ldb + n : 0), valid);
-        }
+      if constexpr (!B_NCONTIG) {
+        const int col = c / CPR, kc = (c % CPR) * CH;
+        const int64_t n = n0 + col, k = k0 + kc;
+        const int valid = (c < BN * CPR && n < args.N && k < args.K) ? int(min<int64_t>(CH, args.K - k)) : 0;
+        rb[i] = load_chunk<false>(B + (valid ? n * args.ldb + k : 0), valid);
+      } else {
+        const int krow = c / CPRN, nc = (c % CPRN) * CH;
+        const int64_t k = k0 + krow, n = n0 + nc;
+        const int valid = (c < BN * CPR && k < args.K && n < args.N) ? int(min<int64_t>(CH, args.N - n)) : 0;
+        rb[i] = load_chunk<false>(B + (valid ? k * args.ldb + n : 0), valid);
       }
     }
   };
@@ -205,7 +238,6 @@ __global__ __launch_bounds__(kThreads) void gemm_fxp_kernel(GemmArgs args) {
         if constexpr (!B_NCONTIG) {
           *reinterpret_cast<uint4*>(bs + (c / CPR) * LDS_K + (c % CPR) * CH) = rb[i];
         } else {
-          constexpr int CPRN = BN / CH;
           const int krow = c / CPRN, nc = (c % CPRN) * CH;
           union {
             uint4 v;
@@ -224,49 +256,51 @@ __global__ __launch_bounds__(kThreads) void gemm_fxp_kernel(GemmArgs args) {
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      P[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) I[i][j][r] = 0;
-    }
 
   const int frag_row = lane & 15, frag_k = (lane >> 4) * (KI / 4);
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
   if (nstages > 0) {
     gload(0);
     lstore(0);
   }
   __syncthreads();
-  for (int s = 0; s < nstages; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nstages) gload(s + 1);
-    const T* as = As + buf * BM * LDS_K + (wm * TL::WM + frag_row) * LDS_K + frag_k;
-    const T* bs = Bs + buf * BN * LDS_K + (wn * TL::WN + frag_row) * LDS_K + frag_k;
+  for (int t = 0; t < ntiles; ++t) {
 #pragma unroll
-    for (int kk = 0; kk < BKS; kk += KI) {
-      Frag fa[MB], fb[NB];
+    for (int st = 0; st < SPT; ++st) {
+      const int s = t * SPT + st;
+      const int buf = s & 1;
+      if (s + 1 < nstages) gload(s + 1);
+      const T* as = As + buf * BM * LDS_K + (wm * TL::WM + frag_row) * LDS_K + frag_k;
+      const T* bs = Bs + buf * BN * LDS_K + (wn * TL::WN + frag_row) * LDS_K + frag_k;
 #pragma unroll
-      for (int i = 0; i < MB; ++i) fa[i] = *reinterpret_cast<const Frag*>(as + i * 16 * LDS_K + kk);
+      for (int kk = 0; kk < BKS; kk += KI) {
+        Frag fa[MB], fb[NB];
 #pragma unroll
-      for (int j = 0; j < NB; ++j) fb[j] = *reinterpret_cast<const Frag*>(bs + j * 16 * LDS_K + kk);
+        for (int i = 0; i < MB; ++i) fa[i] = *reinterpret_cast<const Frag*>(as + i * 16 * LDS_K + kk);
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
+        for (int j = 0; j < NB; ++j) fb[j] = *reinterpret_cast<const Frag*>(bs + j * 16 * LDS_K + kk);
 #pragma unroll
-        for (int j = 0; j < NB; ++j) P[i][j] = M_::mma(fa[i], fb[j], P[i][j]);
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j)  // each tile's chain starts from an all-zero C
+            P[i][j] = M_::mma(fa[i], fb[j], (st == 0 && kk == 0) ? zero4 : P[i][j]);
+      }
+      if (st == SPT - 1) {  // quantisation tile complete
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              I[i][j][r] = wrap_add<BITS>(I[i][j][r], quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
+      }
+      if (s + 1 < nstages) lstore(buf ^ 1);
+      __syncthreads();
     }
-    if (s % SPT == SPT - 1) {  // a quantisation tile is complete
-#pragma unroll
-      for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            I[i][j][r] = wrap_add<BITS>(I[i][j][r], quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
-          P[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    if (s + 1 < nstages) lstore(buf ^ 1);
-    __syncthreads();
   }
 
   // Epilogue. Lane holds rows 4*(lane/16)+r of each 16x16 block, column lane%16.
