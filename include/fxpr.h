@@ -142,6 +142,50 @@ int fxpr_gemm_splits(int64_t m, int64_t n, int64_t k, int io_dtype,
 int64_t fxpr_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k,
                                   int io_dtype, int int_bits, int split_k);
 
+/*
+ * Unified paged prefill + decode attention with fixed-point cross-tile
+ * reductions. q [num_tokens, num_heads, head_dim] and o share io_dtype
+ * (bf16 / f16 / f32) with the caches; k_cache / v_cache are the two halves
+ * of a vLLM [num_blocks, 2, page_size, num_kv_heads, head_dim] cache (any
+ * strides, unit stride along head_dim). Metadata: query_start_loc
+ * [num_requests + 1], seq_lens [num_requests], block_table [num_requests,
+ * max_blocks_per_seq], all int32. alibi_slopes: NULL or num_heads fp32 in
+ * log2 units. softmax_scale_log2 = scale * log2(e); softcap_log2 =
+ * logit_softcap * log2(e) (0 = off); window_size 0 = off. num_splits >= 1
+ * (fxpr_attention_splits() resolves an automatic choice); > 1 needs a
+ * workspace of fxpr_attention_workspace_bytes() bytes (no zeroing needed).
+ * The output is bitwise independent of num_splits, of the batch the request
+ * is in and of max_query_len.
+ * Replaces unified_attention_fxp_run + _attn_fused_kernel /
+ * _attn_split_max_kernel / _attn_split_dv_kernel
+ * (fxpr_vllm/_triton/attention.py:692-953, 127-301, 306-436, 440-652).
+ */
+int fxpr_unified_attention(
+    const void* q, const void* k_cache, const void* v_cache, void* o,
+    int io_dtype, const int32_t* query_start_loc, const int32_t* seq_lens,
+    const int32_t* block_table, const float* alibi_slopes, int num_requests,
+    int64_t num_tokens, int num_heads, int num_kv_heads, int head_dim,
+    int page_size, int max_query_len, int max_blocks_per_seq,
+    int64_t num_blocks, int64_t stride_q_token, int64_t stride_q_head,
+    int64_t stride_k_block, int64_t stride_k_slot, int64_t stride_k_head,
+    int64_t stride_v_block, int64_t stride_v_slot, int64_t stride_v_head,
+    int64_t stride_o_token, int64_t stride_o_head, int64_t stride_bt_row,
+    int is_causal, float softmax_scale_log2, float softcap_log2,
+    int window_size, int int_bits, int frac_bits, int num_splits,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* KV split count for num_kv_splits = requested (0 = automatic).
+ * Replaces _pick_num_splits (fxpr_vllm/_triton/attention.py:664-689). */
+int fxpr_attention_splits(int num_requests, int num_kv_heads, int group,
+                          int max_query_len, int max_blocks_per_seq,
+                          int page_size, int requested);
+
+/* Workspace bytes for a split launch (0 when num_splits <= 1).
+ * Replaces the per-call scratch of attention.py:839-851. */
+int64_t fxpr_attention_workspace_bytes(int64_t num_tokens, int num_heads,
+                                       int head_dim, int int_bits,
+                                       int num_splits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,314 @@
+"""GPU parity: paged attention (HIP/MFMA) vs the oracle and the reference's
+decode / prefill tests (fxpr_vllm/_tests/test_decode.py, test_prefill.py),
+restated.
+
+Within 1e-2 of the oracle on seeded data; bitwise
+identical across KV split counts, batch composition, the decode vs prefill
+path, run-to-run, and whole-tile KV permutations (non-causal).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fxpr_vllm  # noqa: F401
+from oracle import attention as A
+from tests._util import IO_NAME, from_np, to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float16, torch.bfloat16, torch.float32]
+RCP_LN2 = 1.4426950408889634
+
+
+def attend(q, kv, qsl, sl, bt, max_q, splits, *, causal=True, scale=None, alibi=None,
+           bits=32, frac=16, softcap=0.0, window=0):
+    o = torch.empty_like(q)
+    torch.ops.fxpr.unified_attention_fxp(q, kv, o, qsl, sl, bt, int(max_q), alibi, bool(causal),
+                                         scale, bits, frac, float(softcap), int(window), int(splits))
+    return o
+
+
+def oracle(q, kv, qsl, sl, bt, *, causal=True, scale=None, alibi=None, bits=32, frac=16,
+           softcap=0.0, window=0):
+    io = IO_NAME[q.dtype]
+    out = A.unified_attention(to_np(q), to_np(kv), qsl.cpu().numpy(), sl.cpu().numpy(), bt.cpu().numpy(),
+                              io, is_causal=causal, softmax_scale=scale,
+                              alibi_slopes=None if alibi is None else alibi.cpu().numpy(),
+                              int_bits=bits, frac_bits=frac, logit_softcap=softcap, window_size=window)
+    return from_np(out, q.dtype)
+
+
+def decode_case(batch, hq, hkv, d, ctx_lo, ctx_hi, ps, dtype, seed=0, pool_extra=7):
+    g = torch.Generator("cpu").manual_seed(seed)
+    sl = torch.randint(ctx_lo, ctx_hi + 1, (batch,), generator=g, dtype=torch.int32)
+    maxb = int((sl.max().item() + ps - 1) // ps)
+    nb = batch * maxb + pool_extra
+    perm = torch.randperm(nb, generator=g)[: batch * maxb].to(torch.int32)
+    bt = perm.reshape(batch, maxb)
+    q = torch.randn(batch, hq, d, generator=g).to(dtype)
+    kv = torch.randn(nb, 2, ps, hkv, d, generator=g).to(dtype)
+    qsl = torch.arange(batch + 1, dtype=torch.int32)
+    return q.to(DEV), kv.to(DEV), qsl.to(DEV), sl.to(DEV), bt.to(DEV)
+
+
+def prefill_case(seq_lens, hq, hkv, d, dtype, seed=42, scale=1.0):
+    """Contiguous q/k/v into a page-size-1 cache with a per-request block
+    table, like the reference helper prefill_fxp_test
+    (fxpr_vllm/_tests/fixed_point_helpers.py:80-145)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    T = sum(seq_lens)
+    q = (torch.randn(T, hq, d, generator=g) * scale).to(dtype)
+    k = (torch.randn(T, hkv, d, generator=g) * scale).to(dtype)
+    v = (torch.randn(T, hkv, d, generator=g) * scale).to(dtype)
+    kv = torch.empty(T, 2, 1, hkv, d, dtype=dtype)
+    kv[:, 0, 0] = k
+    kv[:, 1, 0] = v
+    maxl = max(seq_lens)
+    bt = torch.zeros(len(seq_lens), maxl, dtype=torch.int32)
+    start = 0
+    for r, L in enumerate(seq_lens):
+        bt[r, :L] = torch.arange(start, start + L, dtype=torch.int32)
+        start += L
+    qsl = torch.tensor([0] + list(np.cumsum(seq_lens)), dtype=torch.int32)
+    sl = torch.tensor(seq_lens, dtype=torch.int32)
+    return (q.to(DEV), kv.to(DEV), qsl.to(DEV), sl.to(DEV), bt.to(DEV)), (q, k, v)
+
+
+def close(got, want, tol=1e-2):
+    g, w = got.double().cpu(), want.double().cpu()
+    return (g - w).abs().max().item() <= tol * max(1.0, w.abs().max().item())
+
+
+# --------------------------------------------------------------------------
+# decode
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_decode_gqa_vs_oracle_and_split_invariance(dtype):
+    q, kv, qsl, sl, bt = decode_case(6, 32, 8, 128, 100, 1500, 16, dtype)
+    ref = attend(q, kv, qsl, sl, bt, 1, 1)
+    for s in (2, 3, 4, 8, 16, 0):
+        assert torch.equal(attend(q, kv, qsl, sl, bt, 1, s), ref), s
+    assert close(ref, oracle(q, kv, qsl, sl, bt))
+
+
+@pytest.mark.parametrize("bits,frac", [(64, 32), (64, 16), (16, 8)])
+def test_decode_fixed_point_formats(bits, frac):
+    q, kv, qsl, sl, bt = decode_case(4, 8, 2, 64, 50, 700, 16, torch.bfloat16, seed=3)
+    ref = attend(q, kv, qsl, sl, bt, 1, 1, bits=bits, frac=frac)
+    assert torch.equal(attend(q, kv, qsl, sl, bt, 1, 5, bits=bits, frac=frac), ref)
+    tol = 1e-2 if bits > 16 else 5e-2  # Q8 in int16 is coarse by design
+    assert close(ref, oracle(q, kv, qsl, sl, bt, bits=bits, frac=frac), tol)
+
+
+@pytest.mark.parametrize("d", [64, 96, 256])
+def test_decode_head_dims(d):
+    q, kv, qsl, sl, bt = decode_case(3, 8, 8, d, 10, 300, 16, torch.bfloat16, seed=d)
+    ref = attend(q, kv, qsl, sl, bt, 1, 1)
+    assert torch.equal(attend(q, kv, qsl, sl, bt, 1, 4), ref)
+    assert close(ref, oracle(q, kv, qsl, sl, bt))
+
+
+# restated: fxpr_vllm/_tests/test_decode.py (4 q heads, 2 kv heads, d 32, page 16,
+# identity block table)
+
+def _ref_decode_inputs(seq_lens, nbps, dtype):
+    g = torch.Generator("cpu").manual_seed(2026)
+    R = len(seq_lens)
+    q = torch.randn(R, 4, 32, generator=g).to(dtype)
+    kv = torch.randn(R * nbps, 2, 16, 2, 32, generator=g).to(dtype)
+    return (q.to(DEV), kv.to(DEV), torch.arange(R + 1, dtype=torch.int32, device=DEV),
+            torch.tensor(seq_lens, dtype=torch.int32, device=DEV),
+            torch.arange(R * nbps, dtype=torch.int32, device=DEV).reshape(R, nbps))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("splits", [1, 2, 4, 8])
+def test_reference_decode_invariant_across_kv_splits(dtype, splits):
+    args = _ref_decode_inputs([160, 96], 10, dtype)
+    o1 = attend(*args, 1, 1, scale=1 / math.sqrt(32))
+    assert torch.equal(o1, attend(*args, 1, splits, scale=1 / math.sqrt(32)))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reference_decode_deterministic_and_native_dtype(dtype):
+    args = _ref_decode_inputs([128, 192, 64], 12, dtype)
+    first = attend(*args, 1, 4, scale=1 / math.sqrt(32))
+    for _ in range(4):
+        assert torch.equal(first, attend(*args, 1, 4, scale=1 / math.sqrt(32)))
+    args = _ref_decode_inputs([48, 32], 3, dtype)
+    o = attend(*args, 1, 4, scale=1 / math.sqrt(32))
+    assert o.dtype == dtype and o.shape == args[0].shape and torch.isfinite(o.float()).all()
+
+
+# --------------------------------------------------------------------------
+# prefill
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("batch,causal", [(1, True), (2, True), (1, False)])
+def test_reference_prefill_correctness(dtype, batch, causal):
+    # fxpr_vllm/_tests/test_prefill.py:97-137
+    lens = [32] * batch
+    args, (q, k, v) = prefill_case(lens, 2, 2, 32, dtype)
+    o = attend(*args, 32, 1, causal=causal, scale=1 / math.sqrt(32))
+    ref = A.attention_reference_fp(q.float().numpy(), k.float().numpy(), v.float().numpy(), lens, causal,
+                                   1 / math.sqrt(32))
+    assert np.allclose(o.float().cpu().numpy(), ref, atol=5e-2, rtol=5e-2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reference_prefill_variable_seq_lens_and_oracle(dtype):
+    # fxpr_vllm/_tests/test_prefill.py:140-158 plus the oracle at 1e-2
+    lens = [70, 128, 100]
+    args, (q, k, v) = prefill_case(lens, 2, 2, 32, dtype, seed=99)
+    o = attend(*args, max(lens), 1, scale=1 / math.sqrt(32))
+    ref = A.attention_reference_fp(q.float().numpy(), k.float().numpy(), v.float().numpy(), lens, True,
+                                   1 / math.sqrt(32))
+    assert np.allclose(o.float().cpu().numpy(), ref, atol=5e-2, rtol=5e-2)
+    assert close(o, oracle(*args, scale=1 / math.sqrt(32)))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("splits", [1, 2, 4, 8])
+def test_reference_prefill_invariant_across_kv_splits(dtype, splits):
+    # fxpr_vllm/_tests/test_prefill.py:161-184
+    args, _ = prefill_case([96, 64], 2, 2, 32, dtype, seed=5)
+    o1 = attend(*args, 96, 1, scale=1 / math.sqrt(32))
+    assert torch.equal(o1, attend(*args, 96, splits, scale=1 / math.sqrt(32)))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reference_prefill_tile_permutation_invariance(dtype):
+    # fxpr_vllm/_tests/test_prefill.py:246-279: permuting whole 64-key tiles
+    L = 192
+    g = torch.Generator("cpu").manual_seed(7)
+    q = torch.randn(L, 2, 32, generator=g) * 0.5
+    k = torch.randn(L, 2, 32, generator=g) * 0.5
+    v = torch.randn(L, 2, 32, generator=g) * 0.5
+    idx = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in (2, 0, 1)])
+
+    def run(kk, vv):
+        kv = torch.empty(L, 2, 1, 2, 32)
+        kv[:, 0, 0], kv[:, 1, 0] = kk, vv
+        bt = torch.arange(L, dtype=torch.int32).reshape(1, L)
+        qsl = torch.tensor([0, L], dtype=torch.int32)
+        sl = torch.tensor([L], dtype=torch.int32)
+        return attend(q.to(dtype).to(DEV), kv.to(dtype).to(DEV), qsl.to(DEV), sl.to(DEV), bt.to(DEV), L, 1,
+                      causal=False, scale=1 / math.sqrt(32))
+
+    assert torch.equal(run(k, v), run(k[idx], v[idx]))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reference_prefill_deterministic(dtype):
+    args, _ = prefill_case([32], 2, 2, 32, dtype, seed=77)
+    r0 = attend(*args, 32, 1, scale=1 / math.sqrt(32))
+    for _ in range(4):
+        assert torch.equal(r0, attend(*args, 32, 1, scale=1 / math.sqrt(32)))
+
+
+# --------------------------------------------------------------------------
+# batch composition and path invariance
+
+
+def test_batch_composition_and_decode_prefill_paths_are_bitwise_identical():
+    dtype = torch.bfloat16
+    g = torch.Generator("cpu").manual_seed(11)
+    hq, hkv, d, ps = 8, 2, 128, 16
+    lens = [300, 77, 1000]
+    nb = sum((L + ps - 1) // ps for L in lens) + 3
+    kv = torch.randn(nb, 2, ps, hkv, d, generator=g).to(dtype).to(DEV)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    tables, off = [], 0
+    for L in lens:
+        n = (L + ps - 1) // ps
+        tables.append(perm[off:off + n])
+        off += n
+    qs = [torch.randn(L, hq, d, generator=g).to(dtype).to(DEV) for L in lens]
+
+    def batch(members):
+        """members: list of (request index, q_len); queries are the last
+        q_len tokens of that request."""
+        q = torch.cat([qs[i][lens[i] - ql:] for i, ql in members])
+        maxb = max(len(tables[i]) for i, _ in members)
+        bt = torch.zeros(len(members), maxb, dtype=torch.int32)
+        for j, (i, _) in enumerate(members):
+            bt[j, :len(tables[i])] = tables[i]
+        qsl = torch.tensor([0] + list(np.cumsum([ql for _, ql in members])), dtype=torch.int32)
+        sl = torch.tensor([lens[i] for i, _ in members], dtype=torch.int32)
+        maxq = max(ql for _, ql in members)
+        return attend(q, kv, qsl.to(DEV), sl.to(DEV), bt.to(DEV), maxq, 0).cpu(), qsl
+
+    full, _ = batch([(0, lens[0])])          # request 0 prefilled entirely
+    dec, _ = batch([(0, 1)])                 # request 0's last token as a decode
+    assert torch.equal(dec[0], full[-1])
+    mixed, qsl = batch([(2, 1), (0, 5), (1, 77)])   # decode + partial prefill + prefill
+    assert torch.equal(mixed[1:6], full[-5:])
+    alone2, _ = batch([(2, 1)])
+    assert torch.equal(mixed[0], alone2[0])
+    big, _ = batch([(1, 1), (2, 1), (0, 1)])
+    assert torch.equal(big[2], dec[0]) and torch.equal(big[1], alone2[0])
+
+
+# --------------------------------------------------------------------------
+# features
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_alibi_softcap_window_vs_oracle(dtype):
+    args, _ = prefill_case([90, 40], 4, 2, 64, dtype, seed=4)
+    slopes = torch.tensor([0.5, 0.25, 0.125, 0.0625], dtype=torch.float32) * RCP_LN2
+    kw = dict(alibi=slopes.to(DEV), softcap=5.0, window=20)
+    o = attend(*args, 90, 1, **kw)
+    assert torch.equal(o, attend(*args, 90, 3, **kw))
+    assert close(o, oracle(*args, alibi=slopes, softcap=5.0, window=20))
+
+
+def test_attention_errors_and_empty():
+    q, kv, qsl, sl, bt = decode_case(2, 4, 2, 32, 10, 40, 16, torch.bfloat16)
+    with pytest.raises(TypeError):
+        attend(q.float(), kv, qsl, sl, bt, 1, 1)
+    with pytest.raises(TypeError):
+        attend(q, kv, qsl.long(), sl, bt, 1, 1)
+    with pytest.raises(ValueError):
+        attend(q, kv[:, 0], qsl, sl, bt, 1, 1)
+    with pytest.raises(ValueError):
+        attend(q, kv, qsl, sl, bt, 1, -1)
+    o = torch.full_like(q, 7.0)
+    torch.ops.fxpr.unified_attention_fxp(q, kv, o, qsl[:1], sl[:0], bt[:0], 1, None, True, None, 32, 16,
+                                         0.0, 0, 1)
+    assert torch.all(o == 7.0)
+
+
+def test_config4_decode_full_shape_properties():
+    # the bench shape: batch 64, 32/8 heads, d 128, ctx U[512, 8192], page 16,
+    # block table from a permutation of a 2^16-block pool; KV generated on
+    # the device. Split invariance for {1, 2, 4, 8, 16} and auto; an oracle
+    # check on three requests.
+    g = torch.Generator("cpu").manual_seed(0)
+    B, hq, hkv, d, ps, pool = 64, 32, 8, 128, 16, 1 << 16
+    sl = torch.randint(512, 8193, (B,), generator=g, dtype=torch.int32)
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    bt = perm[: B * 512].reshape(B, 512)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(DEV)
+    gd = torch.Generator(DEV).manual_seed(1)
+    kv = torch.randn(pool, 2, ps, hkv, d, generator=gd, device=DEV, dtype=torch.bfloat16)
+    qsl = torch.arange(B + 1, dtype=torch.int32, device=DEV)
+    sl_d, bt_d = sl.to(DEV), bt.to(DEV)
+    ref = attend(q, kv, qsl, sl_d, bt_d, 1, 1)
+    for s in (2, 4, 8, 16, 0):
+        assert torch.equal(attend(q, kv, qsl, sl_d, bt_d, 1, s), ref), s
+    for r in (0, 17, 63):
+        nblk = (int(sl[r]) + ps - 1) // ps
+        blocks = bt[r, :nblk].long()
+        sub_kv = kv[blocks.to(DEV)].cpu()
+        sub_bt = torch.arange(nblk, dtype=torch.int32).reshape(1, nblk)
+        want = oracle(q[r:r + 1].cpu(), sub_kv, torch.tensor([0, 1], dtype=torch.int32),
+                      sl[r:r + 1], sub_bt)
+        assert close(ref[r:r + 1], want)

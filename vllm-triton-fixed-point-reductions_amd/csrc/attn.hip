@@ -1,0 +1,131 @@
+// C-ABI entry points of the paged attention (kernels: attn_impl.h,
+// instantiated per input type in attn_{bf16,f16,f32}.hip).
+#include "attn_impl.h"
+
+using namespace fxpr;
+using namespace fxpr::attn;
+
+namespace {
+
+constexpr int kMaxSplits = 64;
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+inline int acc_bytes(int int_bits) { return int_bits == 64 ? 8 : 4; }
+
+int64_t ws_bytes(int64_t num_tokens, int num_heads, int head_dim, int int_bits, int splits) {
+  if (splits <= 1) return 0;
+  const int64_t rows = num_tokens * num_heads * splits;
+  return int64_t(align256(size_t(rows) * 4) + align256(size_t(rows) * acc_bytes(int_bits)) +
+                 align256(size_t(rows) * head_dim * acc_bytes(int_bits)));
+}
+
+}  // namespace
+
+// Split policy of the reference's _pick_num_splits (attention.py:664-689):
+// an explicit request wins; otherwise no split for short contexts (<= 32 key
+// tiles) or when the (request, kv-head, q-tile) workgroups already fill the
+// 256 CUs twice; else a power of two near tiles/32, at most 8.
+extern "C" int fxpr_attention_splits(int num_requests, int num_kv_heads, int group, int max_query_len,
+                                     int max_blocks_per_seq, int page_size, int requested) {
+  if (requested >= 1) return requested > kMaxSplits ? kMaxSplits : requested;
+  const int64_t tiles = cdiv(int64_t(max_blocks_per_seq > 0 ? max_blocks_per_seq : 1) * page_size, TILE);
+  if (tiles <= 32) return 1;
+  const int64_t qtiles = cdiv(int64_t(max_query_len > 1 ? max_query_len : 1) * group, QROWS);
+  const int64_t base = int64_t(num_requests > 1 ? num_requests : 1) * num_kv_heads * qtiles;
+  if (base > 2 * 256) return 1;
+  int64_t s = tiles / 32;
+  if (s > 8) s = 8;
+  if (s < 2) return 1;
+  int p = 1;
+  while (p < s) p <<= 1;
+  return p;
+}
+
+extern "C" int64_t fxpr_attention_workspace_bytes(int64_t num_tokens, int num_heads, int head_dim,
+                                                  int int_bits, int num_splits) {
+  if (num_tokens <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return ws_bytes(num_tokens, num_heads, head_dim, int_bits, num_splits);
+}
+
+extern "C" int fxpr_unified_attention(
+    const void* q, const void* k_cache, const void* v_cache, void* o, int io_dtype,
+    const int32_t* query_start_loc, const int32_t* seq_lens, const int32_t* block_table,
+    const float* alibi_slopes, int num_requests, int64_t num_tokens, int num_heads,
+    int num_kv_heads, int head_dim, int page_size, int max_query_len, int max_blocks_per_seq,
+    int64_t num_blocks, int64_t stride_q_token, int64_t stride_q_head, int64_t stride_k_block,
+    int64_t stride_k_slot, int64_t stride_k_head, int64_t stride_v_block, int64_t stride_v_slot,
+    int64_t stride_v_head, int64_t stride_o_token, int64_t stride_o_head, int64_t stride_bt_row,
+    int is_causal, float softmax_scale_log2, float softcap_log2, int window_size, int int_bits,
+    int frac_bits, int num_splits, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!valid_int_bits(int_bits) || frac_bits < 0 || frac_bits > 63) return FXPR_E_BITS;
+  if (num_requests < 0 || num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      page_size <= 0 || num_splits < 1 || num_heads % num_kv_heads != 0)
+    return FXPR_E_SHAPE;
+  if (num_requests == 0 || num_tokens == 0) return FXPR_OK;
+  if (max_blocks_per_seq <= 0 || num_blocks <= 0) return FXPR_E_SHAPE;
+  if (num_splits > kMaxSplits) return FXPR_E_ARG;
+  if (!q || !k_cache || !v_cache || !o || !query_start_loc || !seq_lens || !block_table) return FXPR_E_ARG;
+  if (io_dtype != FXPR_DTYPE_BF16 && io_dtype != FXPR_DTYPE_F16 && io_dtype != FXPR_DTYPE_F32)
+    return FXPR_E_DTYPE;
+  const int ch = io_dtype == FXPR_DTYPE_F32 ? 4 : 8;
+  // vector loads of q / k / v rows need 16-byte alignment
+  if (head_dim % ch != 0 || head_dim > 256 || (io_dtype == FXPR_DTYPE_F32 && head_dim > 128))
+    return FXPR_E_SHAPE;
+  if (stride_q_token % ch || stride_q_head % ch || stride_k_block % ch || stride_k_slot % ch ||
+      stride_k_head % ch || stride_v_block % ch || stride_v_slot % ch || stride_v_head % ch ||
+      !aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+    return FXPR_E_ARG;
+  if (num_splits > 1 &&
+      (!workspace || workspace_bytes < ws_bytes(num_tokens, num_heads, head_dim, int_bits, num_splits)))
+    return FXPR_E_WORKSPACE;
+
+  AttnArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.o = o;
+  a.qsl = query_start_loc;
+  a.seq_lens = seq_lens;
+  a.bt = block_table;
+  a.alibi = alibi_slopes;
+  if (num_splits > 1) {
+    const int64_t rows = num_tokens * num_heads * num_splits;
+    char* base = static_cast<char*>(workspace);
+    a.pmax = reinterpret_cast<float*>(base);
+    a.den_ws = base + align256(size_t(rows) * 4);
+    a.wv_ws = base + align256(size_t(rows) * 4) + align256(size_t(rows) * acc_bytes(int_bits));
+  }
+  a.sq_t = stride_q_token;
+  a.sq_h = stride_q_head;
+  a.sk_b = stride_k_block;
+  a.sk_s = stride_k_slot;
+  a.sk_h = stride_k_head;
+  a.sv_b = stride_v_block;
+  a.sv_s = stride_v_slot;
+  a.sv_h = stride_v_head;
+  a.so_t = stride_o_token;
+  a.so_h = stride_o_head;
+  a.sbt = stride_bt_row;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_heads / num_kv_heads;
+  a.head_dim = head_dim;
+  a.page_size = page_size;
+  a.num_splits = num_splits;
+  a.window = window_size > 0 ? window_size : 0;
+  a.causal = is_causal ? 1 : 0;
+  a.max_blocks = max_blocks_per_seq;
+  a.num_blocks = num_blocks;
+  a.scale_log2 = softmax_scale_log2;
+  a.softcap_log2 = softcap_log2;
+  a.fxp_scale = pow2f(frac_bits);
+  a.fxp_inv = pow2f(-frac_bits);
+  const int max_qtiles = int(cdiv(int64_t(max_query_len > 1 ? max_query_len : 1) * a.group, QROWS));
+  hipStream_t st = as_stream(stream);
+  switch (io_dtype) {
+    case FXPR_DTYPE_BF16: return run_attn_bf16(a, int_bits, num_requests, max_qtiles, num_tokens, st);
+    case FXPR_DTYPE_F16: return run_attn_f16(a, int_bits, num_requests, max_qtiles, num_tokens, st);
+    default: return run_attn_f32(a, int_bits, num_requests, max_qtiles, num_tokens, st);
+  }
+}

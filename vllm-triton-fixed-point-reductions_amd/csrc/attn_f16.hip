@@ -1,0 +1,17 @@
+// Paged attention kernels instantiated for f16 inputs (see attn_impl.h).
+#include "attn_impl.h"
+
+namespace fxpr {
+namespace attn {
+
+int run_attn_f16(const AttnArgs& a, int bits, int num_requests, int max_qtiles, int64_t num_tokens,
+                hipStream_t st) {
+  switch (bits) {
+    case 16: return dispatch_dmax<FXPR_DTYPE_F16, 16>(a, num_requests, max_qtiles, num_tokens, st);
+    case 32: return dispatch_dmax<FXPR_DTYPE_F16, 32>(a, num_requests, max_qtiles, num_tokens, st);
+    default: return dispatch_dmax<FXPR_DTYPE_F16, 64>(a, num_requests, max_qtiles, num_tokens, st);
+  }
+}
+
+}  // namespace attn
+}  // namespace fxpr

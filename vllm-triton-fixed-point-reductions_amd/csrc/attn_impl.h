@@ -1,0 +1,468 @@
+// Paged prefill + decode attention with fixed-point cross-tile reductions
+// (gfx950 MFMA). Kernels are instantiated per input type in attn_*.hip.
+//
+// Per (request r, query row i, head h), keys n of the request's paged KV:
+//   s_n  = fl32(q . k_n) * scale*log2e  [softcap] [+ alibi*(n - qpos)],
+//          -inf where masked (causal n > qpos, window, n >= seq_len)
+//   m    = max_n s_n over every key of the row (all splits)
+//   w_n  = exp2(s_n - m)
+//   den  = sum_n RNE_sat(w_n * 2^f)                        (integer)
+//   wv_d = sum_tiles RNE_sat(fl32(sum_{n in tile} IO(w_n) v_n[d]) * 2^f)
+//   o_d  = IO(fl32(wv_d) 2^-f / max(fl32(den) 2^-f, 1e-6))
+// Replaces _attn_fused_kernel / _attn_split_max_kernel / _attn_split_dv_kernel
+// (fxpr_vllm/_triton/attention.py:127-301, 306-436, 440-652). Key tiles are
+// aligned to absolute key positions (64 keys for bf16/f16, 32 for f32, the
+// reference's BLOCK_N), and every score and tile partial comes from the same
+// MFMA chain for a given row whatever the workgroup's other rows, the split
+// count or the decode / prefill path, so outputs are bitwise invariant to all
+// of them. Splits exchange only the row maxima (pass 1) and integer partials
+// (pass 2, summed by a combine kernel): no atomics, nothing to pre-zero.
+#pragma once
+
+#include <type_traits>
+
+#include "fxp_device.h"
+#include "fxpr_internal.h"
+
+namespace fxpr {
+namespace attn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;  // 4 waves
+constexpr int TILE = 64;       // keys per iteration (and per split unit)
+constexpr int QROWS = 16;      // query rows (query x GQA head) per workgroup
+
+enum Mode { FUSED = 0, MAXPASS = 1, ACCPASS = 2 };
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  const int32_t* qsl;
+  const int32_t* seq_lens;
+  const int32_t* bt;
+  const float* alibi;  // per q head, already multiplied by log2(e); or null
+  float* pmax;         // [T, Hq, S]
+  void* den_ws;        // [T, Hq, S]     (int32 or int64)
+  void* wv_ws;         // [T, Hq, S, D]  (int32 or int64)
+  int64_t sq_t, sq_h, sk_b, sk_s, sk_h, sv_b, sv_s, sv_h, so_t, so_h, sbt;
+  int num_heads, num_kv_heads, group, head_dim, page_size, num_splits, window, causal;
+  int max_blocks;       // block-table row length
+  int64_t num_blocks;   // physical blocks in the cache
+  float scale_log2, softcap_log2, fxp_scale, fxp_inv;
+};
+
+template <int DT> struct Traits;
+template <> struct Traits<FXPR_DTYPE_BF16> {
+  using T = uint16_t;
+  static constexpr int KI = 32, QUNIT = 64, CH = 8;
+  static __device__ __forceinline__ f32x4 mma(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Traits<FXPR_DTYPE_F16> {
+  using T = uint16_t;
+  static constexpr int KI = 32, QUNIT = 64, CH = 8;
+  static __device__ __forceinline__ f32x4 mma(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Traits<FXPR_DTYPE_F32> {
+  using T = float;
+  static constexpr int KI = 4, QUNIT = 32, CH = 4;
+  static __device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+template <int BITS> struct AccOf { using T = int32_t; };
+template <> struct AccOf<64> { using T = int64_t; };
+
+template <int BITS> __device__ __forceinline__ typename AccOf<BITS>::T wadd(typename AccOf<BITS>::T a, int64_t b) {
+  if constexpr (BITS == 64) return static_cast<int64_t>(static_cast<uint64_t>(a) + static_cast<uint64_t>(b));
+  else return static_cast<int32_t>(static_cast<uint32_t>(a) + static_cast<uint32_t>(b));
+}
+
+template <int BITS> __device__ __forceinline__ float acc_f32(typename AccOf<BITS>::T v, float inv) {
+  if constexpr (BITS == 16) return fixed_to_f32(static_cast<int32_t>(static_cast<int16_t>(v)), inv);
+  else return fixed_to_f32(v, inv);
+}
+
+__device__ __forceinline__ float tanh_approx(float x) {
+  // tanh(x) = sign(x) (1 - 2 / (2^(2|x| log2 e) + 1)); tolerance path only
+  const float e = __builtin_amdgcn_exp2f(2.0f * 1.44269504088896341f * __builtin_fabsf(x));
+  const float t = 1.0f - 2.0f / (e + 1.0f);
+  return x < 0.0f ? -t : t;
+}
+
+// Query-row bookkeeping for one of the workgroup's 16 rows.
+struct RowInfo {
+  int64_t token;
+  int head;
+  int qpos;
+  int kstart, kend;  // valid keys [kstart, kend)
+  bool valid;
+};
+
+__device__ __forceinline__ RowInfo row_info(const AttnArgs& a, int g, int q_start, int q_len, int ctx,
+                                            int seq_len, int row) {
+  RowInfo ri;
+  const int rows_total = q_len * a.group;
+  ri.valid = row < rows_total;
+  const int rr = ri.valid ? row : 0;
+  const int i = rr / a.group, hh = rr % a.group;
+  ri.token = q_start + i;
+  ri.head = g * a.group + hh;
+  ri.qpos = ctx + i;
+  ri.kend = a.causal ? min(seq_len, ri.qpos + 1) : seq_len;
+  ri.kstart = a.window > 0 ? max(0, ri.qpos - a.window + 1) : 0;
+  return ri;
+}
+
+template <int DT, int BITS, int DMAX, int MODE>
+__global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
+  using TR = Traits<DT>;
+  using T = typename TR::T;
+  using AccT = typename AccOf<BITS>::T;
+  constexpr int KI = TR::KI, CH = TR::CH;
+  constexpr int QSTEPS = DMAX / KI;       // MFMAs per 16x16 score block
+  constexpr int DBLK = DMAX / 16;         // 16-wide d blocks of the output
+  constexpr int DB_PER_WAVE = (DBLK + 3) / 4;
+  // LDS pitch of Vt / Ps rows. 16-bit: +8 elements and the key column of Vt
+  // XOR-swizzled by d-chunk (keeps 16-byte fragments contiguous, spreads the
+  // transposing writes over banks); f32: odd pitch, no swizzle.
+  constexpr int VP = DT == FXPR_DTYPE_F32 ? TILE + 1 : TILE + 8;
+  constexpr int QUNIT = TR::QUNIT;
+
+  __shared__ __align__(16) T Vt[DMAX * VP];      // V tile transposed: [d][key]
+  auto vcol = [](int d, int key) -> int {
+    if constexpr (DT == FXPR_DTYPE_F32) return key;
+    else return key ^ (((d >> 3) & 7) << 3);
+  };
+  __shared__ __align__(16) T Ps[QROWS * VP];     // IO-rounded weights: [row][key]
+  __shared__ float red_f[4][QROWS];
+  __shared__ AccT red_i[4][QROWS];
+  __shared__ float row_m[QROWS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.x / a.num_kv_heads, g = blockIdx.x % a.num_kv_heads;
+  const int qt = blockIdx.y, split = blockIdx.z;
+  const int q_start = a.qsl[r];
+  const int q_len = a.qsl[r + 1] - q_start;
+  const int seq_len = a.seq_lens[r];
+  const int ctx = seq_len - q_len;
+  const int rows_total = q_len * a.group;
+  const int row0 = qt * QROWS;
+  if (row0 >= rows_total) return;  // uniform
+
+  // Key range of the workgroup (union over its rows), in absolute tiles.
+  const int i_min = row0 / a.group;
+  const int i_max = min(rows_total - 1, row0 + QROWS - 1) / a.group;
+  const int hi = a.causal ? min(seq_len, ctx + i_max + 1) : seq_len;
+  const int lo = a.window > 0 ? max(0, ctx + i_min - a.window + 1) : 0;
+  const int t_lo = lo / TILE;
+  const int t_hi = hi > lo ? (hi + TILE - 1) / TILE : t_lo;
+  const int ntile = t_hi - t_lo;
+  const int per = (ntile + a.num_splits - 1) / a.num_splits;
+  const int my_lo = (MODE == FUSED) ? t_lo : min(t_hi, t_lo + split * per);
+  const int my_hi = (MODE == FUSED) ? t_hi : min(t_hi, my_lo + per);
+
+  const int32_t* bt_row = a.bt + int64_t(r) * a.sbt;
+  // physical block of key kc (indices clamped so inconsistent metadata can
+  // never address outside the block table or the cache)
+  auto phys_of = [&](int kc) -> int64_t {
+    const int lb = min(kc / a.page_size, a.max_blocks - 1);
+    const int64_t p = bt_row[lb < 0 ? 0 : lb];
+    return p < 0 ? 0 : (p >= a.num_blocks ? a.num_blocks - 1 : p);
+  };
+  const T* Kc = static_cast<const T*>(a.k);
+  const T* Vc = static_cast<const T*>(a.v);
+  const T* Qp = static_cast<const T*>(a.q);
+
+  // Q fragments (MFMA A operand): lane holds row lane%16, its k slots.
+  const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + (lane & 15));
+  const int kg = lane >> 4;  // lane group = MFMA k slot
+  typename std::conditional<DT == FXPR_DTYPE_F32, float, uint4>::type qf[QSTEPS];
+  {
+    const T* qbase = Qp + qrow.token * a.sq_t + int64_t(qrow.head) * a.sq_h;
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) {
+      if constexpr (DT == FXPR_DTYPE_F32) {
+        // step j = 4u + e uses d = 16u + 4*kg + e
+        const int d = 16 * (j >> 2) + 4 * kg + (j & 3);
+        qf[j] = (qrow.valid && d < a.head_dim) ? qbase[d] : 0.0f;
+      } else {
+        const int d = 32 * j + 8 * kg;
+        qf[j] = (qrow.valid && d < a.head_dim) ? *reinterpret_cast<const uint4*>(qbase + d)
+                                                : make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+
+  // Rows held in the score layout: rows 4*kg + e, key lane%16 of the wave's
+  // 16-key block.
+  RowInfo srow[4];
+  float slope[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    srow[e] = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + 4 * kg + e);
+    slope[e] = a.alibi ? a.alibi[srow[e].head] : 0.0f;
+  }
+
+  // Scores of this wave's 16 keys of tile t for the lane's 4 rows.
+  auto scores = [&](int t, float (&s)[4]) {
+    const int key = t * TILE + wave * 16 + (lane & 15);
+    const int kc = max(0, min(key, seq_len - 1));  // clamped: masked below
+    const int64_t phys = phys_of(kc);
+    const T* kp = Kc + phys * a.sk_b + int64_t(kc % a.page_size) * a.sk_s + int64_t(g) * a.sk_h;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) {
+      if constexpr (DT == FXPR_DTYPE_F32) {
+        const int d = 16 * (j >> 2) + 4 * kg + (j & 3);
+        const float kv = d < a.head_dim ? kp[d] : 0.0f;
+        acc = TR::mma(qf[j], kv, acc);
+      } else {
+        const int d = 32 * j + 8 * kg;
+        const uint4 kv = d < a.head_dim ? *reinterpret_cast<const uint4*>(kp + d) : make_uint4(0, 0, 0, 0);
+        acc = TR::mma(qf[j], kv, acc);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = __fmul_rn(acc[e], a.scale_log2);
+      if (a.softcap_log2 > 0.0f) x = a.softcap_log2 * tanh_approx(x / a.softcap_log2);
+      if (a.alibi) x = x + slope[e] * static_cast<float>(key - srow[e].qpos);
+      const bool ok = srow[e].valid && key >= srow[e].kstart && key < srow[e].kend;
+      s[e] = ok ? x : -__builtin_inff();
+    }
+  };
+
+  // ---------------- pass 1: row maxima ----------------
+  float m[4];
+  if constexpr (MODE == FUSED || MODE == MAXPASS) {
+    float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+    for (int t = my_lo; t < my_hi; ++t) {
+      float s[4];
+      scores(t, s);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], s[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o, 64));
+      if ((lane & 15) == 0) red_f[wave][4 * kg + e] = mx[e];
+    }
+    __syncthreads();
+    if constexpr (MODE == MAXPASS) {
+      if (tid < QROWS) {
+        const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
+        const float v = fmaxf(fmaxf(red_f[0][tid], red_f[1][tid]), fmaxf(red_f[2][tid], red_f[3][tid]));
+        if (ri.valid) a.pmax[(ri.token * a.num_heads + ri.head) * a.num_splits + split] = v;
+      }
+      return;
+    }
+    if (tid < QROWS) {
+      const float v = fmaxf(fmaxf(red_f[0][tid], red_f[1][tid]), fmaxf(red_f[2][tid], red_f[3][tid]));
+      row_m[tid] = v;
+    }
+  } else {  // ACCPASS: fold the per-split maxima
+    if (tid < QROWS) {
+      const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
+      float v = -__builtin_inff();
+      if (ri.valid) {
+        const float* pm = a.pmax + (ri.token * a.num_heads + ri.head) * a.num_splits;
+        for (int s2 = 0; s2 < a.num_splits; ++s2) v = fmaxf(v, pm[s2]);
+      }
+      row_m[tid] = v;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float v = row_m[4 * kg + e];
+    m[e] = (srow[e].valid && v != -__builtin_inff()) ? v : 0.0f;  // no key: pin to 0
+  }
+
+  // ---------------- pass 2: integer denominators and weighted V ----------------
+  AccT den[4] = {0, 0, 0, 0};
+  AccT wv[DB_PER_WAVE][4];
+#pragma unroll
+  for (int b = 0; b < DB_PER_WAVE; ++b)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[b][e] = 0;
+
+  constexpr int VCH = DMAX / CH;  // chunks per key row of the V tile
+  for (int t = my_lo; t < my_hi; ++t) {
+    float s[4];
+    scores(t, s);
+    const int kin = wave * 16 + (lane & 15);  // key within the tile
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float w = __builtin_amdgcn_exp2f(s[e] - m[e]);
+      den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
+      Ps[(4 * kg + e) * VP + kin] = Io<DT>::store(w);
+    }
+    // V tile -> LDS, transposed to [d][key]
+#pragma unroll
+    for (int c0 = 0; c0 < TILE * VCH; c0 += kThreads) {
+      const int c = c0 + tid;
+      const int kk = c / VCH, d0 = (c % VCH) * CH;
+      const int key = max(0, min(t * TILE + kk, seq_len - 1));
+      const int64_t phys = phys_of(key);
+      union {
+        uint4 v;
+        T e[CH];
+      } u;
+      u.v = make_uint4(0, 0, 0, 0);
+      if (d0 < a.head_dim)
+        u.v = *reinterpret_cast<const uint4*>(Vc + phys * a.sv_b + int64_t(key % a.page_size) * a.sv_s +
+                                              int64_t(g) * a.sv_h + d0);
+#pragma unroll
+      for (int j = 0; j < CH; ++j) Vt[(d0 + j) * VP + vcol(d0 + j, kk)] = u.e[j];
+    }
+    __syncthreads();
+    // PV: wave handles d blocks wave, wave+4, ...; one quantised chain per
+    // QUNIT keys
+#pragma unroll
+    for (int b = 0; b < DB_PER_WAVE; ++b) {
+      const int db = wave + 4 * b;
+      if (db < DBLK) {
+#pragma unroll
+        for (int u0 = 0; u0 < TILE; u0 += QUNIT) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k0 = 0; k0 < QUNIT; k0 += KI) {
+            if constexpr (DT == FXPR_DTYPE_F32) {
+              const int key = u0 + k0 + kg;
+              const int dv = db * 16 + (lane & 15);
+              acc = TR::mma(Ps[(lane & 15) * VP + key], Vt[dv * VP + vcol(dv, key)], acc);
+            } else {
+              const int key = u0 + k0 + 8 * kg;
+              const int dv = db * 16 + (lane & 15);
+              acc = TR::mma(*reinterpret_cast<const uint4*>(&Ps[(lane & 15) * VP + key]),
+                            *reinterpret_cast<const uint4*>(&Vt[dv * VP + vcol(dv, key)]), acc);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // denominators: sum over the 16 key lanes, then over the waves
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      if constexpr (BITS == 64) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
+      else den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
+    }
+    if ((lane & 15) == 0) red_i[wave][4 * kg + e] = den[e];
+  }
+  __syncthreads();
+
+  // PV layout: lane holds rows 4*kg + e, d = db*16 + lane%16
+  if constexpr (MODE == ACCPASS) {
+    if (tid < QROWS) {
+      const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
+      AccT dsum = wadd<BITS>(wadd<BITS>(red_i[0][tid], red_i[1][tid]), wadd<BITS>(red_i[2][tid], red_i[3][tid]));
+      if (ri.valid) static_cast<AccT*>(a.den_ws)[(ri.token * a.num_heads + ri.head) * a.num_splits + split] = dsum;
+    }
+#pragma unroll
+    for (int b = 0; b < DB_PER_WAVE; ++b) {
+      const int d = (wave + 4 * b) * 16 + (lane & 15);
+      if (wave + 4 * b >= DBLK || d >= a.head_dim) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (!srow[e].valid) continue;
+        AccT* dst = static_cast<AccT*>(a.wv_ws) +
+                    ((srow[e].token * a.num_heads + srow[e].head) * a.num_splits + split) * a.head_dim + d;
+        *dst = wv[b][e];
+      }
+    }
+  } else {  // FUSED: finish here
+    float den_f[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = 4 * kg + e;
+      const AccT dsum = wadd<BITS>(wadd<BITS>(red_i[0][row], red_i[1][row]), wadd<BITS>(red_i[2][row], red_i[3][row]));
+      den_f[e] = fmaxf(acc_f32<BITS>(dsum, a.fxp_inv), 1.0e-6f);
+    }
+    T* Op = static_cast<T*>(a.o);
+#pragma unroll
+    for (int b = 0; b < DB_PER_WAVE; ++b) {
+      const int d = (wave + 4 * b) * 16 + (lane & 15);
+      if (wave + 4 * b >= DBLK || d >= a.head_dim) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (!srow[e].valid) continue;
+        const float num = acc_f32<BITS>(wv[b][e], a.fxp_inv);
+        Op[srow[e].token * a.so_t + int64_t(srow[e].head) * a.so_h + d] = Io<DT>::store(div_rn(num, den_f[e]));
+      }
+    }
+  }
+}
+
+// Sum the per-split integer partials of each (token, head) and divide.
+template <int DT, int BITS>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t num_tokens) {
+  using T = typename Traits<DT>::T;
+  using AccT = typename AccOf<BITS>::T;
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = num_tokens * a.num_heads * a.head_dim;
+  if (idx >= total) return;
+  const int d = int(idx % a.head_dim);
+  const int64_t th = idx / a.head_dim;  // token * Hq + head
+  const AccT* den = static_cast<const AccT*>(a.den_ws) + th * a.num_splits;
+  const AccT* wv = static_cast<const AccT*>(a.wv_ws) + th * a.num_splits * a.head_dim + d;
+  AccT ds = 0, ws = 0;
+  for (int s = 0; s < a.num_splits; ++s) {
+    ds = wadd<BITS>(ds, den[s]);
+    ws = wadd<BITS>(ws, wv[int64_t(s) * a.head_dim]);
+  }
+  const float den_f = fmaxf(acc_f32<BITS>(ds, a.fxp_inv), 1.0e-6f);
+  const int64_t token = th / a.num_heads;
+  const int head = int(th % a.num_heads);
+  static_cast<T*>(a.o)[token * a.so_t + int64_t(head) * a.so_h + d] =
+      Io<DT>::store(div_rn(acc_f32<BITS>(ws, a.fxp_inv), den_f));
+}
+
+template <int DT, int BITS, int DMAX>
+int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st) {
+  dim3 grid(unsigned(num_requests * a.num_kv_heads), unsigned(max_qtiles), 1);
+  if (a.num_splits <= 1) {
+    attn_kernel<DT, BITS, DMAX, FUSED><<<grid, kThreads, 0, st>>>(a);
+    return launch_status();
+  }
+  grid.z = unsigned(a.num_splits);
+  attn_kernel<DT, BITS, DMAX, MAXPASS><<<grid, kThreads, 0, st>>>(a);
+  attn_kernel<DT, BITS, DMAX, ACCPASS><<<grid, kThreads, 0, st>>>(a);
+  const int64_t total = num_tokens * a.num_heads * a.head_dim;
+  attn_combine_kernel<DT, BITS><<<dim3(unsigned(cdiv(total, 256))), 256, 0, st>>>(a, num_tokens);
+  return launch_status();
+}
+
+template <int DT, int BITS>
+int dispatch_dmax(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st) {
+  if (a.head_dim <= 64) return launch_attn<DT, BITS, 64>(a, num_requests, max_qtiles, num_tokens, st);
+  if (a.head_dim <= 128) return launch_attn<DT, BITS, 128>(a, num_requests, max_qtiles, num_tokens, st);
+  if constexpr (DT == FXPR_DTYPE_F32) return FXPR_E_SHAPE;  // fp32 tiles beyond 128 exceed LDS
+  else return launch_attn<DT, BITS, 256>(a, num_requests, max_qtiles, num_tokens, st);
+}
+
+int run_attn_bf16(const AttnArgs& a, int bits, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st);
+int run_attn_f16(const AttnArgs& a, int bits, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st);
+int run_attn_f32(const AttnArgs& a, int bits, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st);
+
+}  // namespace attn
+}  // namespace fxpr

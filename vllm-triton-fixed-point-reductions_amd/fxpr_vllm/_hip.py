@@ -38,10 +38,17 @@ SIGNATURES: dict[str, list] = {
     "fxpr_log_softmax": [_P, _I, _P, _I, _L, _L, _I, _I, _P],
     "fxpr_gemm": [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _P],
     "fxpr_gemm_splits": [_L, _L, _L, _I, _I],
+    "fxpr_unified_attention": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _I, _I, _L,
+                               _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L,
+                               _I, _F, _F, _I, _I, _I, _I, _P, _L, _P],
+    "fxpr_attention_splits": [_I, _I, _I, _I, _I, _I, _I],
 }
 
 # entry points that return something other than an int status
-RESTYPES = {"fxpr_gemm_workspace_bytes": ([_L, _L, _L, _I, _I, _I], _L)}
+RESTYPES = {
+    "fxpr_gemm_workspace_bytes": ([_L, _L, _L, _I, _I, _I], _L),
+    "fxpr_attention_workspace_bytes": ([_L, _I, _I, _I, _I], _L),
+}
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import torch
 
+from ._kernels import attention as _attention
 from ._kernels import casts as _casts
 from ._kernels import gemm as _gemm
 from ._kernels import rows as _rows
@@ -84,6 +85,20 @@ def _gemm_fxp_cuda(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None,
     return _gemm.gemm_fxp_run(a, b, bias, int(fxp_int_bits), int(fxp_frac_bits))
 
 
+def _unified_attention_fxp_cuda(q, kv_cache, o, query_start_loc, seq_lens, block_table,
+                                max_query_len, alibi_slopes, is_causal, softmax_scale,
+                                fxp_int_bits, fxp_frac_bits, logit_softcap, window_size,
+                                num_kv_splits):
+    _check_int_bits(fxp_int_bits)
+    _check_frac_bits(fxp_frac_bits)
+    _attention.unified_attention_fxp_run(
+        q, kv_cache, o, query_start_loc, seq_lens, block_table, int(max_query_len),
+        alibi_slopes, bool(is_causal), None if softmax_scale is None else float(softmax_scale),
+        int(fxp_int_bits), int(fxp_frac_bits), float(logit_softcap), int(window_size),
+        int(num_kv_splits),
+    )
+
+
 def _fixed_row_sum_cuda(q: torch.Tensor, int_bits: int):
     _check_int_bits(int_bits)
     return _rows.fixed_row_sum_run(q, int(int_bits))
@@ -102,5 +117,6 @@ _lib.impl("fixed_to_float", _fixed_to_float_cuda, "CUDA")
 _lib.impl("rms_norm_fxp", _rms_norm_fxp_cuda, "CUDA")
 _lib.impl("rms_norm_fxp_residual", _rms_norm_fxp_residual_cuda, "CUDA")
 _lib.impl("gemm_fxp", _gemm_fxp_cuda, "CUDA")
+_lib.impl("unified_attention_fxp", _unified_attention_fxp_cuda, "CUDA")
 _lib.impl("fixed_row_sum", _fixed_row_sum_cuda, "CUDA")
 _lib.impl("log_softmax_fxp", _log_softmax_fxp_cuda, "CUDA")
