@@ -198,7 +198,52 @@ def wl_gemm(steps, warmup, M, N=128256, K=4096, dtype_name="bf16", int_bits=32, 
     return res
 
 
+def wl_decode(steps, warmup, splits=0, int_bits=32, frac_bits=16, B=64, hq=32, hkv=8, d=128, ps=16,
+              pool=1 << 16, seed=0):
+    """Paged split-K decode attention. Context lengths,
+    the block table (consecutive slices of a permutation of the pool) and q
+    come from a seeded CPU generator; the 4 GiB KV pool from a seeded device
+    generator (generating it on the host would dominate the run)."""
+    import torch
+
+    g = torch.Generator("cpu").manual_seed(seed)
+    sl = torch.randint(512, 8193, (B,), generator=g, dtype=torch.int32)
+    maxb = 8192 // ps
+    bt = torch.randperm(pool, generator=g).to(torch.int32)[: B * maxb].reshape(B, maxb)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to("cuda")
+    key = ("kvpool", pool, ps, hkv, d)
+    if key not in _WEIGHTS:
+        _WEIGHTS.clear()
+        gd = torch.Generator("cuda").manual_seed(seed + 1)
+        _WEIGHTS[key] = torch.randn(pool, 2, ps, hkv, d, generator=gd, device="cuda", dtype=torch.bfloat16)
+    kv = _WEIGHTS[key]
+    qsl = torch.arange(B + 1, dtype=torch.int32, device="cuda")
+    sl_d, bt_d = sl.to("cuda"), bt.to("cuda")
+    o = torch.empty_like(q)
+    scale = 1.0 / d ** 0.5
+
+    def fn():
+        torch.ops.fxpr.unified_attention_fxp(q, kv, o, qsl, sl_d, bt_d, 1, None, True, scale,
+                                             int_bits, frac_bits, 0.0, 0, splits)
+
+    ms = time_op(fn, [()], steps, warmup)
+    sum_l = int(sl.sum())
+    nbytes = sum_l * hkv * d * 2 * 2 + 2 * (B * hq * d * 2) + sum(-(-int(x) // ps) for x in sl) * 4 + 2 * B * 4
+    from fxpr_vllm._kernels import attention as KA
+
+    s_eff = KA.pick_num_splits(splits, B, hkv, hq // hkv, 1, maxb, ps)
+    return {"workload": f"decode attn bf16 B={B} Hq={hq} Hkv={hkv} d={d} ctx~U[512,8192] "
+                        f"(sum {sum_l}) page {ps} splits={s_eff} Q{frac_bits}/i{int_bits}",
+            "ms": round(ms, 5), "bytes": nbytes, "splits": s_eff, "roofline": hbm_roofline(nbytes, ms)}
+
+
 WORKLOADS = {
+    "decode_attn": lambda s, w: wl_decode(s, w, 0),
+    "decode_attn_s1": lambda s, w: wl_decode(s, w, 1),
+    "decode_attn_s2": lambda s, w: wl_decode(s, w, 2),
+    "decode_attn_s4": lambda s, w: wl_decode(s, w, 4),
+    "decode_attn_s8": lambda s, w: wl_decode(s, w, 8),
+    "decode_attn_s16": lambda s, w: wl_decode(s, w, 16),
     "gemm_lm_head": lambda s, w: wl_gemm(s, w, 8192),
     "gemm_lm_head_m2048": lambda s, w: wl_gemm(s, w, 2048),
     "gemm_lm_head_m256": lambda s, w: wl_gemm(s, w, 256),

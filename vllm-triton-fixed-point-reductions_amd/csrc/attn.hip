@@ -116,7 +116,9 @@ extern "C" int fxpr_unified_attention(
   a.window = window_size > 0 ? window_size : 0;
   a.causal = is_causal ? 1 : 0;
   a.max_blocks = max_blocks_per_seq;
+  a.num_requests = num_requests;
   a.num_blocks = num_blocks;
+  a.num_tokens = num_tokens;
   a.scale_log2 = softmax_scale_log2;
   a.softcap_log2 = softcap_log2;
   a.fxp_scale = pow2f(frac_bits);

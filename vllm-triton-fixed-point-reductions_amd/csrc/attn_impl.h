@@ -52,7 +52,9 @@ struct AttnArgs {
   int64_t sq_t, sq_h, sk_b, sk_s, sk_h, sv_b, sv_s, sv_h, so_t, so_h, sbt;
   int num_heads, num_kv_heads, group, head_dim, page_size, num_splits, window, causal;
   int max_blocks;       // block-table row length
+  int num_requests;
   int64_t num_blocks;   // physical blocks in the cache
+  int64_t num_tokens;   // rows of q / o
   float scale_log2, softcap_log2, fxp_scale, fxp_inv;
 };
 
@@ -114,10 +116,12 @@ __device__ __forceinline__ RowInfo row_info(const AttnArgs& a, int g, int q_star
                                             int seq_len, int row) {
   RowInfo ri;
   const int rows_total = q_len * a.group;
-  ri.valid = row < rows_total;
-  const int rr = ri.valid ? row : 0;
+  const int rr = row < rows_total ? row : 0;
   const int i = rr / a.group, hh = rr % a.group;
   ri.token = q_start + i;
+  // rows past the request, or past q / o (inconsistent metadata), are inert
+  ri.valid = row < rows_total && ri.token >= 0 && ri.token < a.num_tokens;
+  if (!ri.valid) ri.token = 0;
   ri.head = g * a.group + hh;
   ri.qpos = ctx + i;
   ri.kend = a.causal ? min(seq_len, ri.qpos + 1) : seq_len;
@@ -419,7 +423,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t n
   using T = typename Traits<DT>::T;
   using AccT = typename AccOf<BITS>::T;
   const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t total = num_tokens * a.num_heads * a.head_dim;
+  // tokens past query_start_loc[num_requests] belong to no request (e.g. graph
+  // padding) and are left untouched, as in the single-pass path
+  const int64_t used = min<int64_t>(num_tokens, a.qsl[a.num_requests]);
+  const int64_t total = used * a.num_heads * a.head_dim;
   if (idx >= total) return;
   const int d = int(idx % a.head_dim);
   const int64_t th = idx / a.head_dim;  // token * Hq + head
