@@ -180,11 +180,16 @@ int fxpr_attention_splits(int num_requests, int num_kv_heads, int group,
                           int max_query_len, int max_blocks_per_seq,
                           int page_size, int requested);
 
-/* Workspace bytes for a split launch (0 when num_splits <= 1).
- * Replaces the per-call scratch of attention.py:839-851. */
+/* Workspace bytes fxpr_unified_attention needs for this launch (0 = none):
+ * per-split maxima and integer partials when num_splits > 1, plus a cache of
+ * the pass-1 scores for decode-shaped launches (max_query_len * group <= 16)
+ * so pass 2 does not re-read K. Replaces the per-call scratch of
+ * attention.py:839-851. */
 int64_t fxpr_attention_workspace_bytes(int64_t num_tokens, int num_heads,
-                                       int head_dim, int int_bits,
-                                       int num_splits);
+                                       int num_kv_heads, int head_dim,
+                                       int int_bits, int num_splits,
+                                       int max_query_len,
+                                       int max_blocks_per_seq, int page_size);
 
 #ifdef __cplusplus
 }

@@ -8,16 +8,42 @@ using namespace fxpr::attn;
 namespace {
 
 constexpr int kMaxSplits = 64;
+constexpr int64_t kScoreCacheMax = int64_t(512) << 20;  // bytes
 
-inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 inline int acc_bytes(int int_bits) { return int_bits == 64 ? 8 : 4; }
 
-int64_t ws_bytes(int64_t num_tokens, int num_heads, int head_dim, int int_bits, int splits) {
-  if (splits <= 1) return 0;
+// Workspace layout: per-split maxima, per-split integer partials (only with
+// more than one split) and the cached pass-1 scores (decode-shaped launches:
+// one 16-row q-tile per (request, kv head), when they fit kScoreCacheMax).
+struct WsLayout {
+  int64_t pmax = -1, den = -1, wv = -1, scores = -1, total = 0;
+};
+
+WsLayout ws_layout(int64_t num_tokens, int num_heads, int num_kv_heads, int head_dim, int int_bits,
+                   int splits, int max_query_len, int max_blocks, int page_size) {
+  WsLayout w;
+  const int group = num_heads / num_kv_heads;
+  const int64_t lmax = int64_t(max_blocks) * page_size;
+  const int64_t score_bytes = num_tokens * num_heads * lmax * 4;
+  const bool cache = int64_t(max_query_len > 1 ? max_query_len : 1) * group <= QROWS &&
+                     score_bytes <= kScoreCacheMax;
+  if (splits <= 1 && !cache) return w;
   const int64_t rows = num_tokens * num_heads * splits;
-  return int64_t(align256(size_t(rows) * 4) + align256(size_t(rows) * acc_bytes(int_bits)) +
-                 align256(size_t(rows) * head_dim * acc_bytes(int_bits)));
+  w.pmax = 0;
+  w.total = align256(rows * 4);
+  if (splits > 1) {
+    w.den = w.total;
+    w.total += align256(rows * acc_bytes(int_bits));
+    w.wv = w.total;
+    w.total += align256(rows * head_dim * acc_bytes(int_bits));
+  }
+  if (cache) {
+    w.scores = w.total;
+    w.total += align256(score_bytes);
+  }
+  return w;
 }
 
 }  // namespace
@@ -42,10 +68,15 @@ extern "C" int fxpr_attention_splits(int num_requests, int num_kv_heads, int gro
   return p;
 }
 
-extern "C" int64_t fxpr_attention_workspace_bytes(int64_t num_tokens, int num_heads, int head_dim,
-                                                  int int_bits, int num_splits) {
-  if (num_tokens <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  return ws_bytes(num_tokens, num_heads, head_dim, int_bits, num_splits);
+extern "C" int64_t fxpr_attention_workspace_bytes(int64_t num_tokens, int num_heads, int num_kv_heads,
+                                                  int head_dim, int int_bits, int num_splits,
+                                                  int max_query_len, int max_blocks_per_seq,
+                                                  int page_size) {
+  if (num_tokens <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0 ||
+      page_size <= 0 || num_heads % num_kv_heads != 0)
+    return 0;
+  return ws_layout(num_tokens, num_heads, num_kv_heads, head_dim, int_bits, num_splits, max_query_len,
+                   max_blocks_per_seq, page_size).total;
 }
 
 extern "C" int fxpr_unified_attention(
@@ -76,9 +107,9 @@ extern "C" int fxpr_unified_attention(
       stride_k_head % ch || stride_v_block % ch || stride_v_slot % ch || stride_v_head % ch ||
       !aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
     return FXPR_E_ARG;
-  if (num_splits > 1 &&
-      (!workspace || workspace_bytes < ws_bytes(num_tokens, num_heads, head_dim, int_bits, num_splits)))
-    return FXPR_E_WORKSPACE;
+  const WsLayout wl = ws_layout(num_tokens, num_heads, num_kv_heads, head_dim, int_bits, num_splits,
+                                max_query_len, max_blocks_per_seq, page_size);
+  if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return FXPR_E_WORKSPACE;
 
   AttnArgs a{};
   a.q = q;
@@ -89,13 +120,11 @@ extern "C" int fxpr_unified_attention(
   a.seq_lens = seq_lens;
   a.bt = block_table;
   a.alibi = alibi_slopes;
-  if (num_splits > 1) {
-    const int64_t rows = num_tokens * num_heads * num_splits;
-    char* base = static_cast<char*>(workspace);
-    a.pmax = reinterpret_cast<float*>(base);
-    a.den_ws = base + align256(size_t(rows) * 4);
-    a.wv_ws = base + align256(size_t(rows) * 4) + align256(size_t(rows) * acc_bytes(int_bits));
-  }
+  char* base = static_cast<char*>(workspace);
+  if (wl.pmax >= 0) a.pmax = reinterpret_cast<float*>(base + wl.pmax);
+  if (wl.den >= 0) a.den_ws = base + wl.den;
+  if (wl.wv >= 0) a.wv_ws = base + wl.wv;
+  if (wl.scores >= 0) a.scores = reinterpret_cast<float*>(base + wl.scores);
   a.sq_t = stride_q_token;
   a.sq_h = stride_q_head;
   a.sk_b = stride_k_block;
@@ -119,6 +148,8 @@ extern "C" int fxpr_unified_attention(
   a.num_requests = num_requests;
   a.num_blocks = num_blocks;
   a.num_tokens = num_tokens;
+  a.lmax = int64_t(max_blocks_per_seq) * page_size;
+  a.ps_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz(unsigned(page_size)) : -1;
   a.scale_log2 = softmax_scale_log2;
   a.softcap_log2 = softcap_log2;
   a.fxp_scale = pow2f(frac_bits);

@@ -35,7 +35,7 @@ constexpr int kThreads = 256;  // 4 waves
 constexpr int TILE = 64;       // keys per iteration (and per split unit)
 constexpr int QROWS = 16;      // query rows (query x GQA head) per workgroup
 
-enum Mode { FUSED = 0, MAXPASS = 1, ACCPASS = 2 };
+enum Mode { FUSED = 0, MAXPASS = 1, ACCPASS = 2, ACCCACHED = 3 };
 
 struct AttnArgs {
   const void* q;
@@ -47,6 +47,7 @@ struct AttnArgs {
   const int32_t* bt;
   const float* alibi;  // per q head, already multiplied by log2(e); or null
   float* pmax;         // [T, Hq, S]
+  float* scores;       // [T, Hq, lmax] cached pass-1 scores, or null
   void* den_ws;        // [T, Hq, S]     (int32 or int64)
   void* wv_ws;         // [T, Hq, S, D]  (int32 or int64)
   int64_t sq_t, sq_h, sk_b, sk_s, sk_h, sv_b, sv_s, sv_h, so_t, so_h, sbt;
@@ -55,6 +56,8 @@ struct AttnArgs {
   int num_requests;
   int64_t num_blocks;   // physical blocks in the cache
   int64_t num_tokens;   // rows of q / o
+  int64_t lmax;         // key capacity of a block-table row (max_blocks * page_size)
+  int ps_shift;         // log2(page_size) if a power of two, else -1
   float scale_log2, softcap_log2, fxp_scale, fxp_inv;
 };
 
@@ -134,6 +137,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   using TR = Traits<DT>;
   using T = typename TR::T;
   using AccT = typename AccOf<BITS>::T;
+  using KFrag = typename std::conditional<DT == FXPR_DTYPE_F32, float, uint4>::type;
   constexpr int KI = TR::KI, CH = TR::CH;
   constexpr int QSTEPS = DMAX / KI;       // MFMAs per 16x16 score block
   constexpr int DBLK = DMAX / 16;         // 16-wide d blocks of the output
@@ -143,19 +147,34 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   // transposing writes over banks); f32: odd pitch, no swizzle.
   constexpr int VP = DT == FXPR_DTYPE_F32 ? TILE + 1 : TILE + 8;
   constexpr int QUNIT = TR::QUNIT;
+  constexpr int VCH = DMAX / CH;                    // 16-byte chunks per key row of a V tile
+  constexpr int VITER = TILE * VCH / kThreads;      // V chunks per thread per tile
 
-  __shared__ __align__(16) T Vt[DMAX * VP];      // V tile transposed: [d][key]
+  // V tile in LDS. f32: transposed [d][key]. 16-bit: natural [key][d] (row
+  // pitch VNP), turned into MFMA B operands by ds_read_b64_tr_b16.
+  constexpr bool TR16 = DT != FXPR_DTYPE_F32;
+  constexpr int VNP = DMAX + 16;
+  __shared__ __align__(16) T Vt[TR16 ? TILE * VNP : DMAX * VP];
+  __shared__ __align__(16) T Ps[QROWS * VP]; // IO-rounded weights: [row][key]
+  __shared__ float red_f[4][QROWS];
+  __shared__ AccT red_i[4][QROWS];
+  __shared__ float row_m[QROWS];
   auto vcol = [](int d, int key) -> int {
     if constexpr (DT == FXPR_DTYPE_F32) return key;
     else return key ^ (((d >> 3) & 7) << 3);
   };
-  __shared__ __align__(16) T Ps[QROWS * VP];     // IO-rounded weights: [row][key]
-  __shared__ float red_f[4][QROWS];
-  __shared__ AccT red_i[4][QROWS];
-  __shared__ float row_m[QROWS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = blockIdx.x / a.num_kv_heads, g = blockIdx.x % a.num_kv_heads;
+  // The hardware deals consecutive workgroup ids to the 8 XCDs round-robin.
+  // Remap so the kv heads of one request (which share every KV page) run back
+  // to back on one XCD and read each page's head rows close together in time.
+  int logical;
+  {
+    const int bid = blockIdx.x, nblk = gridDim.x;
+    const int q8 = nblk >> 3, r8 = nblk & 7, x = bid & 7, i = bid >> 3;
+    logical = x < r8 ? x * (q8 + 1) + i : r8 * (q8 + 1) + (x - r8) * q8 + i;
+  }
+  const int r = logical / a.num_kv_heads, g = logical % a.num_kv_heads;
   const int qt = blockIdx.y, split = blockIdx.z;
   const int q_start = a.qsl[r];
   const int q_len = a.qsl[r + 1] - q_start;
@@ -163,7 +182,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   const int ctx = seq_len - q_len;
   const int rows_total = q_len * a.group;
   const int row0 = qt * QROWS;
-  if (row0 >= rows_total) return;  // uniform
+  if (row0 >= rows_total || seq_len <= 0) return;  // uniform
 
   // Key range of the workgroup (union over its rows), in absolute tiles.
   const int i_min = row0 / a.group;
@@ -174,26 +193,35 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   const int t_hi = hi > lo ? (hi + TILE - 1) / TILE : t_lo;
   const int ntile = t_hi - t_lo;
   const int per = (ntile + a.num_splits - 1) / a.num_splits;
+  constexpr bool PASS2 = MODE == ACCPASS || MODE == ACCCACHED;
   const int my_lo = (MODE == FUSED) ? t_lo : min(t_hi, t_lo + split * per);
   const int my_hi = (MODE == FUSED) ? t_hi : min(t_hi, my_lo + per);
+  const bool cached = a.scores != nullptr;
 
   const int32_t* bt_row = a.bt + int64_t(r) * a.sbt;
-  // physical block of key kc (indices clamped so inconsistent metadata can
-  // never address outside the block table or the cache)
-  auto phys_of = [&](int kc) -> int64_t {
-    const int lb = min(kc / a.page_size, a.max_blocks - 1);
-    const int64_t p = bt_row[lb < 0 ? 0 : lb];
-    return p < 0 ? 0 : (p >= a.num_blocks ? a.num_blocks - 1 : p);
-  };
   const T* Kc = static_cast<const T*>(a.k);
   const T* Vc = static_cast<const T*>(a.v);
   const T* Qp = static_cast<const T*>(a.q);
+  const int kg = lane >> 4;  // lane group = MFMA k slot
+
+  // Paged addressing. Keys are clamped to [0, seq_len) and block-table /
+  // block indices to their ranges, so inconsistent metadata can never address
+  // outside the table or the cache (such keys are masked anyway).
+  auto clamp_key = [&](int key) { return max(0, min(key, seq_len - 1)); };
+  auto bt_entry = [&](int key) -> int {
+    const int lb = a.ps_shift >= 0 ? (key >> a.ps_shift) : key / a.page_size;
+    return bt_row[min(lb, a.max_blocks - 1)];
+  };
+  auto row_addr = [&](int key, int entry, int64_t sb, int64_t ss, int64_t sh) -> int64_t {
+    const int64_t p = entry < 0 ? 0 : (entry >= a.num_blocks ? a.num_blocks - 1 : entry);
+    const int slot = a.ps_shift >= 0 ? (key & (a.page_size - 1)) : key % a.page_size;
+    return p * sb + int64_t(slot) * ss + int64_t(g) * sh;
+  };
 
   // Q fragments (MFMA A operand): lane holds row lane%16, its k slots.
-  const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + (lane & 15));
-  const int kg = lane >> 4;  // lane group = MFMA k slot
-  typename std::conditional<DT == FXPR_DTYPE_F32, float, uint4>::type qf[QSTEPS];
+  KFrag qf[QSTEPS];
   {
+    const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + (lane & 15));
     const T* qbase = Qp + qrow.token * a.sq_t + int64_t(qrow.head) * a.sq_h;
 #pragma unroll
     for (int j = 0; j < QSTEPS; ++j) {
@@ -219,25 +247,29 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     slope[e] = a.alibi ? a.alibi[srow[e].head] : 0.0f;
   }
 
-  // Scores of this wave's 16 keys of tile t for the lane's 4 rows.
-  auto scores = [&](int t, float (&s)[4]) {
-    const int key = t * TILE + wave * 16 + (lane & 15);
-    const int kc = max(0, min(key, seq_len - 1));  // clamped: masked below
-    const int64_t phys = phys_of(kc);
-    const T* kp = Kc + phys * a.sk_b + int64_t(kc % a.page_size) * a.sk_s + int64_t(g) * a.sk_h;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // K fragments of the lane's key of tile t (key clamped, bt entry given).
+  auto k_load = [&](int t, int entry, KFrag (&kf)[QSTEPS]) {
+    const int key = clamp_key(t * TILE + wave * 16 + (lane & 15));
+    const T* kp = Kc + row_addr(key, entry, a.sk_b, a.sk_s, a.sk_h);
 #pragma unroll
     for (int j = 0; j < QSTEPS; ++j) {
       if constexpr (DT == FXPR_DTYPE_F32) {
         const int d = 16 * (j >> 2) + 4 * kg + (j & 3);
-        const float kv = d < a.head_dim ? kp[d] : 0.0f;
-        acc = TR::mma(qf[j], kv, acc);
+        kf[j] = d < a.head_dim ? kp[d] : 0.0f;
       } else {
         const int d = 32 * j + 8 * kg;
-        const uint4 kv = d < a.head_dim ? *reinterpret_cast<const uint4*>(kp + d) : make_uint4(0, 0, 0, 0);
-        acc = TR::mma(qf[j], kv, acc);
+        kf[j] = d < a.head_dim ? *reinterpret_cast<const uint4*>(kp + d) : make_uint4(0, 0, 0, 0);
       }
     }
+  };
+  auto k_entry = [&](int t) { return bt_entry(clamp_key(t * TILE + wave * 16 + (lane & 15))); };
+
+  // Scaled, transformed, masked log2-space scores of tile t.
+  auto k_scores = [&](int t, const KFrag (&kf)[QSTEPS], float (&s)[4]) {
+    const int key = t * TILE + wave * 16 + (lane & 15);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) acc = TR::mma(qf[j], kf[j], acc);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float x = __fmul_rn(acc[e], a.scale_log2);
@@ -248,15 +280,38 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     }
   };
 
-  // ---------------- pass 1: row maxima ----------------
+  // Cached scores: [T, Hq, lmax] fp32, written by pass 1, read by pass 2.
+  auto sc_addr = [&](int e, int key) -> float* {
+    return a.scores + (srow[e].token * a.num_heads + srow[e].head) * a.lmax + key;
+  };
+
+  // ---------------- pass 1: row maxima (and cached scores) ----------------
   float m[4];
   if constexpr (MODE == FUSED || MODE == MAXPASS) {
     float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
-    for (int t = my_lo; t < my_hi; ++t) {
-      float s[4];
-      scores(t, s);
+    if (my_lo < my_hi) {
+      KFrag kcur[QSTEPS], knxt[QSTEPS];
+      k_load(my_lo, k_entry(my_lo), kcur);
+      int e_nxt = k_entry(min(my_lo + 1, my_hi - 1));
+      for (int t = my_lo; t < my_hi; ++t) {
+        if (t + 1 < my_hi) k_load(t + 1, e_nxt, knxt);             // next tile in flight
+        const int e_n2 = k_entry(min(t + 2, my_hi - 1));            // and its successor's page
+        float s[4];
+        k_scores(t, kcur, s);
+        if (MODE == MAXPASS && cached) {
+          const int key = t * TILE + wave * 16 + (lane & 15);
+          if (key < min(seq_len, a.lmax)) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], s[e]);
+            for (int e = 0; e < 4; ++e)
+              if (srow[e].valid) *sc_addr(e, key) = s[e];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], s[e]);
+#pragma unroll
+        for (int j = 0; j < QSTEPS; ++j) kcur[j] = knxt[j];
+        e_nxt = e_n2;
+      }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -277,7 +332,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
       const float v = fmaxf(fmaxf(red_f[0][tid], red_f[1][tid]), fmaxf(red_f[2][tid], red_f[3][tid]));
       row_m[tid] = v;
     }
-  } else {  // ACCPASS: fold the per-split maxima
+  } else {  // pass 2 only: fold the per-split maxima
     if (tid < QROWS) {
       const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
       float v = -__builtin_inff();
@@ -303,80 +358,159 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) wv[b][e] = 0;
 
-  constexpr int VCH = DMAX / CH;  // chunks per key row of the V tile
-  for (int t = my_lo; t < my_hi; ++t) {
-    float s[4];
-    scores(t, s);
-    const int kin = wave * 16 + (lane & 15);  // key within the tile
+  constexpr bool from_cache = MODE == ACCCACHED;
+  // V chunk c = i*256 + tid of a tile: key c / VCH, d chunk (c % VCH) * CH
+  auto v_entries = [&](int t, int (&ve)[VITER]) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float w = __builtin_amdgcn_exp2f(s[e] - m[e]);
-      den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
-      Ps[(4 * kg + e) * VP + kin] = Io<DT>::store(w);
+    for (int i = 0; i < VITER; ++i) ve[i] = bt_entry(clamp_key(t * TILE + (i * kThreads + tid) / VCH));
+  };
+  auto v_load = [&](int t, const int (&ve)[VITER], uint4 (&vr)[VITER]) {
+#pragma unroll
+    for (int i = 0; i < VITER; ++i) {
+      const int c = i * kThreads + tid;
+      const int key = clamp_key(t * TILE + c / VCH), d0 = (c % VCH) * CH;
+      vr[i] = d0 < a.head_dim ? *reinterpret_cast<const uint4*>(Vc + row_addr(key, ve[i], a.sv_b, a.sv_s, a.sv_h) + d0)
+                              : make_uint4(0, 0, 0, 0);
     }
-    // V tile -> LDS, transposed to [d][key]
+  };
+  auto s_load = [&](int t, float (&s)[4]) {
+    const int key = t * TILE + wave * 16 + (lane & 15);
 #pragma unroll
-    for (int c0 = 0; c0 < TILE * VCH; c0 += kThreads) {
-      const int c = c0 + tid;
-      const int kk = c / VCH, d0 = (c % VCH) * CH;
-      const int key = max(0, min(t * TILE + kk, seq_len - 1));
-      const int64_t phys = phys_of(key);
-      union {
-        uint4 v;
-        T e[CH];
-      } u;
-      u.v = make_uint4(0, 0, 0, 0);
-      if (d0 < a.head_dim)
-        u.v = *reinterpret_cast<const uint4*>(Vc + phys * a.sv_b + int64_t(key % a.page_size) * a.sv_s +
-                                              int64_t(g) * a.sv_h + d0);
-#pragma unroll
-      for (int j = 0; j < CH; ++j) Vt[(d0 + j) * VP + vcol(d0 + j, kk)] = u.e[j];
+    for (int e = 0; e < 4; ++e)
+      s[e] = (srow[e].valid && key >= srow[e].kstart && key < srow[e].kend && key < a.lmax) ? *sc_addr(e, key)
+                                                                                         : -__builtin_inff();
+  };
+
+  if (my_lo < my_hi) {
+    int ve_cur[VITER], ve_nxt[VITER];
+    uint4 vr_cur[VITER], vr_nxt[VITER];
+    KFrag kcur[QSTEPS], knxt[QSTEPS];
+    float sc_cur[4], sc_nxt[4];
+    int ke_nxt = 0;
+    v_entries(my_lo, ve_cur);
+    v_load(my_lo, ve_cur, vr_cur);
+    v_entries(min(my_lo + 1, my_hi - 1), ve_nxt);
+    if (from_cache) {
+      s_load(my_lo, sc_cur);
+    } else {
+      k_load(my_lo, k_entry(my_lo), kcur);
+      ke_nxt = k_entry(min(my_lo + 1, my_hi - 1));
     }
-    __syncthreads();
-    // PV: wave handles d blocks wave, wave+4, ...; one quantised chain per
-    // QUNIT keys
+    for (int t = my_lo; t < my_hi; ++t) {
+      const bool more = t + 1 < my_hi;
+      // issue the next tile's loads before working on this one
+      int ve_n2[VITER];
+      int ke_n2 = 0;
+      if (more) {
+        v_load(t + 1, ve_nxt, vr_nxt);
+        if (from_cache) s_load(t + 1, sc_nxt);
+        else k_load(t + 1, ke_nxt, knxt);
+      }
+      v_entries(min(t + 2, my_hi - 1), ve_n2);
+      if (!from_cache) ke_n2 = k_entry(min(t + 2, my_hi - 1));
+
+      float s[4];
+      if (from_cache) {
 #pragma unroll
-    for (int b = 0; b < DB_PER_WAVE; ++b) {
-      const int db = wave + 4 * b;
-      if (db < DBLK) {
+        for (int e = 0; e < 4; ++e) s[e] = sc_cur[e];
+      } else {
+        k_scores(t, kcur, s);
+      }
+      const int kin = wave * 16 + (lane & 15);  // key within the tile
 #pragma unroll
-        for (int u0 = 0; u0 < TILE; u0 += QUNIT) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int e = 0; e < 4; ++e) {
+        const float w = __builtin_amdgcn_exp2f(s[e] - m[e]);
+        den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
+        Ps[(4 * kg + e) * VP + kin] = Io<DT>::store(w);
+      }
 #pragma unroll
-          for (int k0 = 0; k0 < QUNIT; k0 += KI) {
-            if constexpr (DT == FXPR_DTYPE_F32) {
-              const int key = u0 + k0 + kg;
-              const int dv = db * 16 + (lane & 15);
-              acc = TR::mma(Ps[(lane & 15) * VP + key], Vt[dv * VP + vcol(dv, key)], acc);
-            } else {
-              const int key = u0 + k0 + 8 * kg;
-              const int dv = db * 16 + (lane & 15);
-              acc = TR::mma(*reinterpret_cast<const uint4*>(&Ps[(lane & 15) * VP + key]),
-                            *reinterpret_cast<const uint4*>(&Vt[dv * VP + vcol(dv, key)]), acc);
+      for (int i = 0; i < VITER; ++i) {  // V tile -> LDS
+        const int c = i * kThreads + tid;
+        const int kk = c / VCH, d0 = (c % VCH) * CH;
+        if constexpr (TR16) {
+          *reinterpret_cast<uint4*>(&Vt[kk * VNP + d0]) = vr_cur[i];
+        } else {  // transposed to [d][key]
+          union {
+            uint4 v;
+            T e[CH];
+          } u;
+          u.v = vr_cur[i];
+#pragma unroll
+          for (int j = 0; j < CH; ++j) Vt[(d0 + j) * VP + vcol(d0 + j, kk)] = u.e[j];
+        }
+      }
+      __syncthreads();
+      // PV: wave handles d blocks wave, wave+4, ...; one quantised chain per
+      // QUNIT keys
+#pragma unroll
+      for (int b = 0; b < DB_PER_WAVE; ++b) {
+        const int db = wave + 4 * b;
+        if (db < DBLK) {
+          const int dv = db * 16 + (lane & 15);
+#pragma unroll
+          for (int u0 = 0; u0 < TILE; u0 += QUNIT) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k0 = 0; k0 < QUNIT; k0 += KI) {
+              if constexpr (DT == FXPR_DTYPE_F32) {
+                const int key = u0 + k0 + kg;
+                acc = TR::mma(Ps[(lane & 15) * VP + key], Vt[dv * VP + vcol(dv, key)], acc);
+              } else {
+                // B operand: lane (kg, i) needs V[keys key..key+7][d = db*16 + i].
+                // ds_read_b64_tr_b16 gives lane i of each 16-lane group
+                // element (i % 4) of source lane 4c' + i/4, c' = 0..3; source
+                // lane j points at V[key0 + j/4][db*16 + 4*(j%4)].
+                const int key = u0 + k0 + 8 * kg;
+                const int j = lane & 15;
+                typedef short v4s __attribute__((ext_vector_type(4)));
+                const T* src = &Vt[(key + (j >> 2)) * VNP + db * 16 + 4 * (j & 3)];
+                const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) v4s*)(src));
+                const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) v4s*)(src + 4 * VNP));
+                struct {
+                  v4s a, b;
+                } both = {lo4, hi4};
+                acc = TR::mma(*reinterpret_cast<const uint4*>(&Ps[(lane & 15) * VP + key]),
+                              __builtin_bit_cast(uint4, both), acc);
+              }
             }
-          }
 #pragma unroll
-          for (int e = 0; e < 4; ++e) wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+            for (int e = 0; e < 4; ++e)
+              wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+          }
+        }
+      }
+      __syncthreads();
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < VITER; ++i) {
+          vr_cur[i] = vr_nxt[i];
+          ve_nxt[i] = ve_n2[i];
+        }
+        if (from_cache) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc_cur[e] = sc_nxt[e];
+        } else {
+#pragma unroll
+          for (int j = 0; j < QSTEPS; ++j) kcur[j] = knxt[j];
+          ke_nxt = ke_n2;
         }
       }
     }
-    __syncthreads();
   }
 
   // denominators: sum over the 16 key lanes, then over the waves
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      if constexpr (BITS == 64) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
-      else den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
-    }
+    for (int o = 1; o < 16; o <<= 1) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
     if ((lane & 15) == 0) red_i[wave][4 * kg + e] = den[e];
   }
   __syncthreads();
 
   // PV layout: lane holds rows 4*kg + e, d = db*16 + lane%16
-  if constexpr (MODE == ACCPASS) {
+  if (PASS2 && a.num_splits > 1) {
     if (tid < QROWS) {
       const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
       AccT dsum = wadd<BITS>(wadd<BITS>(red_i[0][tid], red_i[1][tid]), wadd<BITS>(red_i[2][tid], red_i[3][tid]));
@@ -394,7 +528,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         *dst = wv[b][e];
       }
     }
-  } else {  // FUSED: finish here
+  } else {  // single split: finish here
     float den_f[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -446,16 +580,18 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t n
 
 template <int DT, int BITS, int DMAX>
 int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st) {
-  dim3 grid(unsigned(num_requests * a.num_kv_heads), unsigned(max_qtiles), 1);
-  if (a.num_splits <= 1) {
+  dim3 grid(unsigned(num_requests * a.num_kv_heads), unsigned(max_qtiles), unsigned(a.num_splits));
+  if (a.num_splits <= 1 && a.scores == nullptr) {
     attn_kernel<DT, BITS, DMAX, FUSED><<<grid, kThreads, 0, st>>>(a);
     return launch_status();
   }
-  grid.z = unsigned(a.num_splits);
   attn_kernel<DT, BITS, DMAX, MAXPASS><<<grid, kThreads, 0, st>>>(a);
-  attn_kernel<DT, BITS, DMAX, ACCPASS><<<grid, kThreads, 0, st>>>(a);
-  const int64_t total = num_tokens * a.num_heads * a.head_dim;
-  attn_combine_kernel<DT, BITS><<<dim3(unsigned(cdiv(total, 256))), 256, 0, st>>>(a, num_tokens);
+  if (a.scores) attn_kernel<DT, BITS, DMAX, ACCCACHED><<<grid, kThreads, 0, st>>>(a);
+  else attn_kernel<DT, BITS, DMAX, ACCPASS><<<grid, kThreads, 0, st>>>(a);
+  if (a.num_splits > 1) {
+    const int64_t total = num_tokens * a.num_heads * a.head_dim;
+    attn_combine_kernel<DT, BITS><<<dim3(unsigned(cdiv(total, 256))), 256, 0, st>>>(a, num_tokens);
+  }
   return launch_status();
 }
 

@@ -99,8 +99,9 @@ def unified_attention_fxp_run(
     splits = pick_num_splits(num_kv_splits, num_requests, num_kv_heads, group,
                              int(max_query_len), max_blocks, page_size)
     lib = _hip.load()
-    ws_bytes = lib.fxpr_attention_workspace_bytes(num_tokens, num_heads, head_dim,
-                                                  int(fxp_int_bits), splits)
+    ws_bytes = lib.fxpr_attention_workspace_bytes(num_tokens, num_heads, num_kv_heads, head_dim,
+                                                  int(fxp_int_bits), splits, int(max_query_len),
+                                                  max_blocks, page_size)
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes > 0 else None
     _hip.call(
         "fxpr_unified_attention",
