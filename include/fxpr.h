@@ -151,9 +151,10 @@ int64_t fxpr_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k,
  * [num_requests + 1], seq_lens [num_requests], block_table [num_requests,
  * max_blocks_per_seq], all int32. alibi_slopes: NULL or num_heads fp32 in
  * log2 units. softmax_scale_log2 = scale * log2(e); softcap_log2 =
- * logit_softcap * log2(e) (0 = off); window_size 0 = off. num_splits >= 1
- * (fxpr_attention_splits() resolves an automatic choice); > 1 needs a
- * workspace of fxpr_attention_workspace_bytes() bytes (no zeroing needed).
+ * logit_softcap * log2(e) (0 = off); window_size 0 = off. num_kv_splits:
+ * 0 = automatic (fxpr_attention_splits() reports the choice), >= 1 = that
+ * many KV splits. The launch needs a workspace of
+ * fxpr_attention_workspace_bytes() bytes when that is non-zero (no zeroing).
  * The output is bitwise independent of num_splits, of the batch the request
  * is in and of max_query_len.
  * Replaces unified_attention_fxp_run + _attn_fused_kernel /
@@ -171,7 +172,7 @@ int fxpr_unified_attention(
     int64_t stride_v_block, int64_t stride_v_slot, int64_t stride_v_head,
     int64_t stride_o_token, int64_t stride_o_head, int64_t stride_bt_row,
     int is_causal, float softmax_scale_log2, float softcap_log2,
-    int window_size, int int_bits, int frac_bits, int num_splits,
+    int window_size, int int_bits, int frac_bits, int num_kv_splits,
     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* KV split count for num_kv_splits = requested (0 = automatic).
@@ -185,10 +186,10 @@ int fxpr_attention_splits(int num_requests, int num_kv_heads, int group,
  * the pass-1 scores for decode-shaped launches (max_query_len * group <= 16)
  * so pass 2 does not re-read K. Replaces the per-call scratch of
  * attention.py:839-851. */
-int64_t fxpr_attention_workspace_bytes(int64_t num_tokens, int num_heads,
-                                       int num_kv_heads, int head_dim,
-                                       int int_bits, int num_splits,
-                                       int max_query_len,
+int64_t fxpr_attention_workspace_bytes(int num_requests, int64_t num_tokens,
+                                       int num_heads, int num_kv_heads,
+                                       int head_dim, int int_bits,
+                                       int num_kv_splits, int max_query_len,
                                        int max_blocks_per_seq, int page_size);
 
 #ifdef __cplusplus

@@ -48,34 +48,53 @@ WsLayout ws_layout(int64_t num_tokens, int num_heads, int num_kv_heads, int head
 
 }  // namespace
 
-// Split policy of the reference's _pick_num_splits (attention.py:664-689):
-// an explicit request wins; otherwise no split for short contexts (<= 32 key
-// tiles) or when the (request, kv-head, q-tile) workgroups already fill the
-// 256 CUs twice; else a power of two near tiles/32, at most 8.
-extern "C" int fxpr_attention_splits(int num_requests, int num_kv_heads, int group, int max_query_len,
-                                     int max_blocks_per_seq, int page_size, int requested) {
-  if (requested >= 1) return requested > kMaxSplits ? kMaxSplits : requested;
-  const int64_t tiles = cdiv(int64_t(max_blocks_per_seq > 0 ? max_blocks_per_seq : 1) * page_size, TILE);
-  if (tiles <= 32) return 1;
+// Split policy. An explicit request wins (key tiles dealt evenly over the
+// splits, as the reference's _split_tile_range does). Automatic (0), after
+// the reference's _pick_num_splits (attention.py:664-689): no split for short
+// contexts (<= 32 key tiles) or when the (request, kv-head, q-tile)
+// workgroups already oversubscribe the 256 CUs; otherwise splits of a fixed
+// kSplitTiles key tiles each, so every workgroup carries about the same work
+// whatever its request's length (requests shorter than the longest get empty
+// splits, which only write neutral partials). Split counts never change bits.
+namespace {
+constexpr int kSplitTiles = 16;
+
+struct SplitPlan {
+  int splits, tiles_per_split;
+};
+
+SplitPlan plan_splits(int num_requests, int num_kv_heads, int group, int max_query_len, int max_blocks,
+                      int page_size, int requested) {
+  if (requested >= 1) return {requested > kMaxSplits ? kMaxSplits : requested, 0};
+  const int64_t tiles = cdiv(int64_t(max_blocks > 0 ? max_blocks : 1) * page_size, TILE);
+  if (tiles <= 32) return {1, 0};
   const int64_t qtiles = cdiv(int64_t(max_query_len > 1 ? max_query_len : 1) * group, QROWS);
   const int64_t base = int64_t(num_requests > 1 ? num_requests : 1) * num_kv_heads * qtiles;
-  if (base > 2 * 256) return 1;
-  int64_t s = tiles / 32;
-  if (s > 8) s = 8;
-  if (s < 2) return 1;
-  int p = 1;
-  while (p < s) p <<= 1;
-  return p;
+  if (base > 8 * 256) return {1, 0};
+  int64_t s = cdiv(tiles, kSplitTiles);
+  if (s > kMaxSplits) s = kMaxSplits;
+  const int per = int(cdiv(tiles, s));
+  return {int(s), per};
+}
+}  // namespace
+
+extern "C" int fxpr_attention_splits(int num_requests, int num_kv_heads, int group, int max_query_len,
+                                     int max_blocks_per_seq, int page_size, int requested) {
+  return plan_splits(num_requests, num_kv_heads, group, max_query_len, max_blocks_per_seq, page_size,
+                     requested)
+      .splits;
 }
 
-extern "C" int64_t fxpr_attention_workspace_bytes(int64_t num_tokens, int num_heads, int num_kv_heads,
-                                                  int head_dim, int int_bits, int num_splits,
-                                                  int max_query_len, int max_blocks_per_seq,
-                                                  int page_size) {
-  if (num_tokens <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0 ||
-      page_size <= 0 || num_heads % num_kv_heads != 0)
+extern "C" int64_t fxpr_attention_workspace_bytes(int num_requests, int64_t num_tokens, int num_heads,
+                                                  int num_kv_heads, int head_dim, int int_bits,
+                                                  int num_kv_splits, int max_query_len,
+                                                  int max_blocks_per_seq, int page_size) {
+  if (num_requests <= 0 || num_tokens <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      max_blocks_per_seq <= 0 || page_size <= 0 || num_heads % num_kv_heads != 0 || num_kv_splits < 0)
     return 0;
-  return ws_layout(num_tokens, num_heads, num_kv_heads, head_dim, int_bits, num_splits, max_query_len,
+  const SplitPlan sp = plan_splits(num_requests, num_kv_heads, num_heads / num_kv_heads, max_query_len,
+                                   max_blocks_per_seq, page_size, num_kv_splits);
+  return ws_layout(num_tokens, num_heads, num_kv_heads, head_dim, int_bits, sp.splits, max_query_len,
                    max_blocks_per_seq, page_size).total;
 }
 
@@ -88,14 +107,16 @@ extern "C" int fxpr_unified_attention(
     int64_t stride_k_slot, int64_t stride_k_head, int64_t stride_v_block, int64_t stride_v_slot,
     int64_t stride_v_head, int64_t stride_o_token, int64_t stride_o_head, int64_t stride_bt_row,
     int is_causal, float softmax_scale_log2, float softcap_log2, int window_size, int int_bits,
-    int frac_bits, int num_splits, void* workspace, int64_t workspace_bytes, void* stream) {
+    int frac_bits, int num_kv_splits, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!valid_int_bits(int_bits) || frac_bits < 0 || frac_bits > 63) return FXPR_E_BITS;
   if (num_requests < 0 || num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
-      page_size <= 0 || num_splits < 1 || num_heads % num_kv_heads != 0)
+      page_size <= 0 || num_kv_splits < 0 || num_heads % num_kv_heads != 0)
     return FXPR_E_SHAPE;
   if (num_requests == 0 || num_tokens == 0) return FXPR_OK;
   if (max_blocks_per_seq <= 0 || num_blocks <= 0) return FXPR_E_SHAPE;
-  if (num_splits > kMaxSplits) return FXPR_E_ARG;
+  const SplitPlan sp = plan_splits(num_requests, num_kv_heads, num_heads / num_kv_heads, max_query_len,
+                                   max_blocks_per_seq, page_size, num_kv_splits);
+  const int num_splits = sp.splits;
   if (!q || !k_cache || !v_cache || !o || !query_start_loc || !seq_lens || !block_table) return FXPR_E_ARG;
   if (io_dtype != FXPR_DTYPE_BF16 && io_dtype != FXPR_DTYPE_F16 && io_dtype != FXPR_DTYPE_F32)
     return FXPR_E_DTYPE;
@@ -142,6 +163,7 @@ extern "C" int fxpr_unified_attention(
   a.head_dim = head_dim;
   a.page_size = page_size;
   a.num_splits = num_splits;
+  a.tiles_per_split = sp.tiles_per_split;
   a.window = window_size > 0 ? window_size : 0;
   a.causal = is_causal ? 1 : 0;
   a.max_blocks = max_blocks_per_seq;

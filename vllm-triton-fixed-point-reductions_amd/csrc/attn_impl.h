@@ -53,6 +53,7 @@ struct AttnArgs {
   int64_t sq_t, sq_h, sk_b, sk_s, sk_h, sv_b, sv_s, sv_h, so_t, so_h, sbt;
   int num_heads, num_kv_heads, group, head_dim, page_size, num_splits, window, causal;
   int max_blocks;       // block-table row length
+  int tiles_per_split;  // > 0: fixed key tiles per split (work-balanced); 0: even division
   int num_requests;
   int64_t num_blocks;   // physical blocks in the cache
   int64_t num_tokens;   // rows of q / o
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   const int t_lo = lo / TILE;
   const int t_hi = hi > lo ? (hi + TILE - 1) / TILE : t_lo;
   const int ntile = t_hi - t_lo;
-  const int per = (ntile + a.num_splits - 1) / a.num_splits;
+  const int per = a.tiles_per_split > 0 ? a.tiles_per_split : (ntile + a.num_splits - 1) / a.num_splits;
   constexpr bool PASS2 = MODE == ACCPASS || MODE == ACCCACHED;
   const int my_lo = (MODE == FUSED) ? t_lo : min(t_hi, t_lo + split * per);
   const int my_hi = (MODE == FUSED) ? t_hi : min(t_hi, my_lo + per);
@@ -290,14 +291,18 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   if constexpr (MODE == FUSED || MODE == MAXPASS) {
     float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
     if (my_lo < my_hi) {
-      KFrag kcur[QSTEPS], knxt[QSTEPS];
-      k_load(my_lo, k_entry(my_lo), kcur);
-      int e_nxt = k_entry(min(my_lo + 1, my_hi - 1));
-      for (int t = my_lo; t < my_hi; ++t) {
-        if (t + 1 < my_hi) k_load(t + 1, e_nxt, knxt);             // next tile in flight
-        const int e_n2 = k_entry(min(t + 2, my_hi - 1));            // and its successor's page
+      // Ping-pong K buffers, loop unrolled by two: the loads for tile t + 1
+      // are in flight while tile t is scored, and no register copy ever
+      // touches a buffer whose loads are outstanding (that would force a wait
+      // on them).
+      KFrag kA[QSTEPS], kB[QSTEPS];
+      k_load(my_lo, k_entry(my_lo), kA);
+      int e_next = k_entry(min(my_lo + 1, my_hi - 1));
+      auto step = [&](int t, const KFrag (&cur)[QSTEPS], KFrag (&nxt)[QSTEPS]) {
+        if (t + 1 < my_hi) k_load(t + 1, e_next, nxt);
+        e_next = k_entry(min(t + 2, my_hi - 1));
         float s[4];
-        k_scores(t, kcur, s);
+        k_scores(t, cur, s);
         if (MODE == MAXPASS && cached) {
           const int key = t * TILE + wave * 16 + (lane & 15);
           if (key < min(seq_len, a.lmax)) {
@@ -308,9 +313,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], s[e]);
-#pragma unroll
-        for (int j = 0; j < QSTEPS; ++j) kcur[j] = knxt[j];
-        e_nxt = e_n2;
+      };
+      for (int t = my_lo; t < my_hi; t += 2) {
+        step(t, kA, kB);
+        if (t + 1 < my_hi) step(t + 1, kB, kA);
       }
     }
 #pragma unroll
@@ -382,35 +388,38 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   };
 
   if (my_lo < my_hi) {
-    int ve_cur[VITER], ve_nxt[VITER];
-    uint4 vr_cur[VITER], vr_nxt[VITER];
-    KFrag kcur[QSTEPS], knxt[QSTEPS];
-    float sc_cur[4], sc_nxt[4];
-    int ke_nxt = 0;
-    v_entries(my_lo, ve_cur);
-    v_load(my_lo, ve_cur, vr_cur);
-    v_entries(min(my_lo + 1, my_hi - 1), ve_nxt);
-    if (from_cache) {
-      s_load(my_lo, sc_cur);
+    // Ping-pong buffers, unrolled by two (see pass 1): V chunks, their page
+    // entries (fetched two tiles ahead), and K fragments or cached scores.
+    int veA[VITER], veB[VITER];
+    uint4 vrA[VITER], vrB[VITER];
+    KFrag kA[QSTEPS], kB[QSTEPS];
+    float scA[4], scB[4];
+    int ke_next = 0;
+    v_entries(my_lo, veA);
+    v_load(my_lo, veA, vrA);
+    v_entries(min(my_lo + 1, my_hi - 1), veB);
+    if constexpr (from_cache) {
+      s_load(my_lo, scA);
     } else {
-      k_load(my_lo, k_entry(my_lo), kcur);
-      ke_nxt = k_entry(min(my_lo + 1, my_hi - 1));
+      k_load(my_lo, k_entry(my_lo), kA);
+      ke_next = k_entry(min(my_lo + 1, my_hi - 1));
     }
-    for (int t = my_lo; t < my_hi; ++t) {
-      const bool more = t + 1 < my_hi;
-      // issue the next tile's loads before working on this one
-      int ve_n2[VITER];
-      int ke_n2 = 0;
-      if (more) {
+    // ve_nxt holds the entries of tile t + 1 on entry; refilled with t + 3's
+    // entries... entries of tile t + 2 go to ve_cur's array once its tile is
+    // loaded.
+    auto step = [&](int t, const uint4 (&vr_cur)[VITER], uint4 (&vr_nxt)[VITER], int (&ve_cur)[VITER],
+                    const int (&ve_nxt)[VITER], const KFrag (&kcur)[QSTEPS], KFrag (&knxt)[QSTEPS],
+                    const float (&sc_cur)[4], float (&sc_nxt)[4]) {
+      if (t + 1 < my_hi) {
         v_load(t + 1, ve_nxt, vr_nxt);
-        if (from_cache) s_load(t + 1, sc_nxt);
-        else k_load(t + 1, ke_nxt, knxt);
+        if constexpr (from_cache) s_load(t + 1, sc_nxt);
+        else k_load(t + 1, ke_next, knxt);
       }
-      v_entries(min(t + 2, my_hi - 1), ve_n2);
-      if (!from_cache) ke_n2 = k_entry(min(t + 2, my_hi - 1));
+      v_entries(min(t + 2, my_hi - 1), ve_cur);  // ve_cur's tile is loaded: reuse it for t + 2
+      if constexpr (!from_cache) ke_next = k_entry(min(t + 2, my_hi - 1));
 
       float s[4];
-      if (from_cache) {
+      if constexpr (from_cache) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) s[e] = sc_cur[e];
       } else {
@@ -482,21 +491,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         }
       }
       __syncthreads();
-      if (more) {
-#pragma unroll
-        for (int i = 0; i < VITER; ++i) {
-          vr_cur[i] = vr_nxt[i];
-          ve_nxt[i] = ve_n2[i];
-        }
-        if (from_cache) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sc_cur[e] = sc_nxt[e];
-        } else {
-#pragma unroll
-          for (int j = 0; j < QSTEPS; ++j) kcur[j] = knxt[j];
-          ke_nxt = ke_n2;
-        }
-      }
+    };
+    for (int t = my_lo; t < my_hi; t += 2) {
+      step(t, vrA, vrB, veA, veB, kA, kB, scA, scB);
+      if (t + 1 < my_hi) step(t + 1, vrB, vrA, veB, veA, kB, kA, scB, scA);
     }
   }
 

@@ -47,7 +47,7 @@ SIGNATURES: dict[str, list] = {
 # entry points that return something other than an int status
 RESTYPES = {
     "fxpr_gemm_workspace_bytes": ([_L, _L, _L, _I, _I, _I], _L),
-    "fxpr_attention_workspace_bytes": ([_L, _I, _I, _I, _I, _I, _I, _I, _I], _L),
+    "fxpr_attention_workspace_bytes": ([_I, _L, _I, _I, _I, _I, _I, _I, _I, _I], _L),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -95,13 +95,10 @@ def unified_attention_fxp_run(
     ss_log2 = float(ss) * _RCP_LN2
     softcap_log2 = float(logit_softcap) * _RCP_LN2 if float(logit_softcap) > 0.0 else 0.0
     max_blocks = bt.shape[1]
-    group = num_heads // num_kv_heads
-    splits = pick_num_splits(num_kv_splits, num_requests, num_kv_heads, group,
-                             int(max_query_len), max_blocks, page_size)
     lib = _hip.load()
-    ws_bytes = lib.fxpr_attention_workspace_bytes(num_tokens, num_heads, num_kv_heads, head_dim,
-                                                  int(fxp_int_bits), splits, int(max_query_len),
-                                                  max_blocks, page_size)
+    ws_bytes = lib.fxpr_attention_workspace_bytes(num_requests, num_tokens, num_heads, num_kv_heads,
+                                                  head_dim, int(fxp_int_bits), int(num_kv_splits),
+                                                  int(max_query_len), max_blocks, page_size)
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes > 0 else None
     _hip.call(
         "fxpr_unified_attention",
@@ -112,7 +109,7 @@ def unified_attention_fxp_run(
         q.stride(0), q.stride(1), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         v_cache.stride(0), v_cache.stride(1), v_cache.stride(2), out.stride(0), out.stride(1),
         bt.stride(0), int(bool(is_causal)), ss_log2, softcap_log2, max(0, int(window_size)),
-        int(fxp_int_bits), int(fxp_frac_bits), splits, _hip.ptr(ws), ws_bytes,
+        int(fxp_int_bits), int(fxp_frac_bits), int(num_kv_splits), _hip.ptr(ws), ws_bytes,
         _hip.stream_ptr(q.device),
     )
     if out is not o:
