@@ -128,6 +128,9 @@ extern "C" int fxpr_unified_attention(
       stride_k_head % ch || stride_v_block % ch || stride_v_slot % ch || stride_v_head % ch ||
       !aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
     return FXPR_E_ARG;
+  // the kernels form cache offsets as 32 x 32 -> 64-bit products
+  for (int64_t sv : {stride_k_block, stride_k_slot, stride_k_head, stride_v_block, stride_v_slot, stride_v_head})
+    if (sv < 0 || sv > int64_t(0xffffffff)) return FXPR_E_ARG;
   const WsLayout wl = ws_layout(num_tokens, num_heads, num_kv_heads, head_dim, int_bits, num_splits,
                                 max_query_len, max_blocks_per_seq, page_size);
   if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return FXPR_E_WORKSPACE;
@@ -145,7 +148,10 @@ extern "C" int fxpr_unified_attention(
   if (wl.pmax >= 0) a.pmax = reinterpret_cast<float*>(base + wl.pmax);
   if (wl.den >= 0) a.den_ws = base + wl.den;
   if (wl.wv >= 0) a.wv_ws = base + wl.wv;
-  if (wl.scores >= 0) a.scores = reinterpret_cast<float*>(base + wl.scores);
+  if (wl.scores >= 0) {
+    a.scores = reinterpret_cast<float*>(base + wl.scores);
+    a.score_bytes = int(num_tokens * num_heads * int64_t(max_blocks_per_seq) * page_size * 4);
+  }
   a.sq_t = stride_q_token;
   a.sq_h = stride_q_head;
   a.sk_b = stride_k_block;

@@ -30,10 +30,15 @@ namespace attn {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 16 bytes as a native vector (HIP's uint4 is a struct whose copies can
+// become memcpys that keep arrays of them out of registers)
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;  // 4 waves
 constexpr int TILE = 64;       // keys per iteration (and per split unit)
 constexpr int QROWS = 16;      // query rows (query x GQA head) per workgroup
+// Word 3 of a raw (untyped, unswizzled) buffer resource on gfx9-family GPUs.
+constexpr int kBufferWord3 = 0x00020000;
 
 enum Mode { FUSED = 0, MAXPASS = 1, ACCPASS = 2, ACCCACHED = 3 };
 
@@ -59,6 +64,7 @@ struct AttnArgs {
   int64_t num_tokens;   // rows of q / o
   int64_t lmax;         // key capacity of a block-table row (max_blocks * page_size)
   int ps_shift;         // log2(page_size) if a power of two, else -1
+  int score_bytes;      // size of the score cache (< 2^31), or 0
   float scale_log2, softcap_log2, fxp_scale, fxp_inv;
 };
 
@@ -66,7 +72,7 @@ template <int DT> struct Traits;
 template <> struct Traits<FXPR_DTYPE_BF16> {
   using T = uint16_t;
   static constexpr int KI = 32, QUNIT = 64, CH = 8;
-  static __device__ __forceinline__ f32x4 mma(uint4 a, uint4 b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
@@ -74,7 +80,7 @@ template <> struct Traits<FXPR_DTYPE_BF16> {
 template <> struct Traits<FXPR_DTYPE_F16> {
   using T = uint16_t;
   static constexpr int KI = 32, QUNIT = 64, CH = 8;
-  static __device__ __forceinline__ f32x4 mma(uint4 a, uint4 b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
@@ -138,7 +144,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   using TR = Traits<DT>;
   using T = typename TR::T;
   using AccT = typename AccOf<BITS>::T;
-  using KFrag = typename std::conditional<DT == FXPR_DTYPE_F32, float, uint4>::type;
+  using KFrag = typename std::conditional<DT == FXPR_DTYPE_F32, float, u32x4>::type;
   constexpr int KI = TR::KI, CH = TR::CH;
   constexpr int QSTEPS = DMAX / KI;       // MFMAs per 16x16 score block
   constexpr int DBLK = DMAX / 16;         // 16-wide d blocks of the output
@@ -166,15 +172,11 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // The hardware deals consecutive workgroup ids to the 8 XCDs round-robin.
-  // Remap so the kv heads of one request (which share every KV page) run back
-  // to back on one XCD and read each page's head rows close together in time.
-  int logical;
-  {
-    const int bid = blockIdx.x, nblk = gridDim.x;
-    const int q8 = nblk >> 3, r8 = nblk & 7, x = bid & 7, i = bid >> 3;
-    logical = x < r8 ? x * (q8 + 1) + i : r8 * (q8 + 1) + (x - r8) * q8 + i;
-  }
+  // The hardware deals consecutive workgroup ids to the 8 XCDs round-robin,
+  // so the kv heads of one request (which share every KV page) run at the
+  // same time, one per XCD, and every XCD gets a share of every request:
+  // the XCDs stay balanced whatever the spread of context lengths.
+  const int logical = blockIdx.x;
   const int r = logical / a.num_kv_heads, g = logical % a.num_kv_heads;
   const int qt = blockIdx.y, split = blockIdx.z;
   const int q_start = a.qsl[r];
@@ -213,10 +215,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     const int lb = a.ps_shift >= 0 ? (key >> a.ps_shift) : key / a.page_size;
     return bt_row[min(lb, a.max_blocks - 1)];
   };
-  auto row_addr = [&](int key, int entry, int64_t sb, int64_t ss, int64_t sh) -> int64_t {
-    const int64_t p = entry < 0 ? 0 : (entry >= a.num_blocks ? a.num_blocks - 1 : entry);
-    const int slot = a.ps_shift >= 0 ? (key & (a.page_size - 1)) : key % a.page_size;
-    return p * sb + int64_t(slot) * ss + int64_t(g) * sh;
+  // Element offsets as 32 x 32 -> 64-bit products (the host guarantees
+  // cache strides below 2^32): a full 64 x 64 product is expanded with an
+  // undefined high half that can land on a register with a load in flight,
+  // and reading it would wait for that load.
+  const int last_block = int(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
+  auto row_addr = [&](int key, int entry, int64_t sb, int64_t ss, int64_t sh) -> uint64_t {
+    const uint32_t p = uint32_t(entry < 0 ? 0 : min(entry, last_block));
+    const uint32_t slot = uint32_t(a.ps_shift >= 0 ? (key & (a.page_size - 1)) : key % a.page_size);
+    return uint64_t(p) * uint32_t(sb) + uint64_t(slot) * uint32_t(ss) + uint64_t(uint32_t(g)) * uint32_t(sh);
   };
 
   // Q fragments (MFMA A operand): lane holds row lane%16, its k slots.
@@ -232,8 +239,8 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         qf[j] = (qrow.valid && d < a.head_dim) ? qbase[d] : 0.0f;
       } else {
         const int d = 32 * j + 8 * kg;
-        qf[j] = (qrow.valid && d < a.head_dim) ? *reinterpret_cast<const uint4*>(qbase + d)
-                                                : make_uint4(0, 0, 0, 0);
+        qf[j] = (qrow.valid && d < a.head_dim) ? *reinterpret_cast<const u32x4*>(qbase + d)
+                                                : u32x4{0u, 0u, 0u, 0u};
       }
     }
   }
@@ -249,6 +256,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   }
 
   // K fragments of the lane's key of tile t (key clamped, bt entry given).
+  // Every load is issued unconditionally: loads under a branch would leave
+  // the compiler unable to count outstanding loads, and it would then wait
+  // for all of them. Columns past head_dim read column 0 of the same key;
+  // their products vanish because the Q fragments there are zero.
   auto k_load = [&](int t, int entry, KFrag (&kf)[QSTEPS]) {
     const int key = clamp_key(t * TILE + wave * 16 + (lane & 15));
     const T* kp = Kc + row_addr(key, entry, a.sk_b, a.sk_s, a.sk_h);
@@ -256,10 +267,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     for (int j = 0; j < QSTEPS; ++j) {
       if constexpr (DT == FXPR_DTYPE_F32) {
         const int d = 16 * (j >> 2) + 4 * kg + (j & 3);
-        kf[j] = d < a.head_dim ? kp[d] : 0.0f;
+        kf[j] = kp[d < a.head_dim ? d : 0];
       } else {
         const int d = 32 * j + 8 * kg;
-        kf[j] = d < a.head_dim ? *reinterpret_cast<const uint4*>(kp + d) : make_uint4(0, 0, 0, 0);
+        kf[j] = *reinterpret_cast<const u32x4*>(kp + (d < a.head_dim ? d : 0));
       }
     }
   };
@@ -282,41 +293,72 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   };
 
   // Cached scores: [T, Hq, lmax] fp32, written by pass 1, read by pass 2.
-  auto sc_addr = [&](int e, int key) -> float* {
-    return a.scores + (srow[e].token * a.num_heads + srow[e].head) * a.lmax + key;
-  };
+  // Row bases of the lane's four rows; rows outside the request point at a
+  // real row of the workgroup (pass 2 reads the same cache lines as that
+  // row and discards the values; pass 1 never stores them).
+  float* sbase[4] = {nullptr, nullptr, nullptr, nullptr};
+  uint32_t soff[4] = {0u, 0u, 0u, 0u};  // byte offsets of the rows
+  if (cached && (MODE == MAXPASS || MODE == ACCCACHED)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      RowInfo rr = srow[e];
+      if (!rr.valid) rr = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + min(e, rows_total - row0 - 1));
+      const int64_t idx = (rr.token * a.num_heads + rr.head) * a.lmax;
+      sbase[e] = a.scores + idx;
+      soff[e] = uint32_t(idx * 4);
+    }
+  }
 
   // ---------------- pass 1: row maxima (and cached scores) ----------------
   float m[4];
   if constexpr (MODE == FUSED || MODE == MAXPASS) {
     float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
     if (my_lo < my_hi) {
-      // Ping-pong K buffers, loop unrolled by two: the loads for tile t + 1
-      // are in flight while tile t is scored, and no register copy ever
-      // touches a buffer whose loads are outstanding (that would force a wait
-      // on them).
-      KFrag kA[QSTEPS], kB[QSTEPS];
-      k_load(my_lo, k_entry(my_lo), kA);
-      int e_next = k_entry(min(my_lo + 1, my_hi - 1));
-      auto step = [&](int t, const KFrag (&cur)[QSTEPS], KFrag (&nxt)[QSTEPS]) {
-        if (t + 1 < my_hi) k_load(t + 1, e_next, nxt);
-        e_next = k_entry(min(t + 2, my_hi - 1));
-        float s[4];
-        k_scores(t, cur, s);
-        if (MODE == MAXPASS && cached) {
-          const int key = t * TILE + wave * 16 + (lane & 15);
-          if (key < min(seq_len, a.lmax)) {
+      // Ring of R1 K buffers: tiles t+1 .. t+R1-1 are in flight while tile t
+      // is scored. The page entry of a tile is loaded R1 steps before its K
+      // rows, so waiting for an entry never waits for recent K loads (loads
+      // complete in issue order). Buffers are indexed by compile-time slots
+      // of the R1-times unrolled loop, so no register copy touches a buffer
+      // with loads in flight. The loop body has no branches and issues the
+      // same memory instructions every step, so the compiler can count the
+      // loads in flight exactly: tiles past my_hi are loaded clamped (cache
+      // hits) and scored as fully masked, and the cached-score stores go
+      // through a buffer resource, with an out-of-range offset (dropped by
+      // the hardware) where a lane has nothing to store.
+      constexpr int R1 = 2;
+      KFrag kb[R1][QSTEPS];
+      int eb[R1];
+      auto tl = [&](int x) { return min(x, my_hi - 1); };
+      const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(a.scores, 0, a.score_bytes, kBufferWord3);
+      const int kmax = min(seq_len, int(a.lmax < 0x7fffffff ? a.lmax : 0x7fffffff));
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (srow[e].valid) *sc_addr(e, key) = s[e];
+      for (int i = 0; i < R1; ++i) eb[i] = k_entry(tl(my_lo + i));
+#pragma unroll
+      for (int i = 0; i + 1 < R1; ++i) {
+        k_load(tl(my_lo + i), eb[i], kb[i]);
+        eb[i] = k_entry(tl(my_lo + R1 + i));
+      }
+      for (int t = my_lo; t < my_hi; t += R1) {
+#pragma unroll
+        for (int u = 0; u < R1; ++u) {
+          const int sl = (u + R1 - 1) % R1;
+          k_load(tl(t + u + R1 - 1), eb[sl], kb[sl]);
+          eb[sl] = k_entry(tl(t + u + 2 * R1 - 1));
+          const bool live = t + u < my_hi;
+          float s[4];
+          k_scores(t + u, kb[u], s);
+          const int key = (t + u) * TILE + wave * 16 + (lane & 15);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s[e] = live ? s[e] : -__builtin_inff();
+            if (MODE == MAXPASS && cached) {
+              const bool st = live && srow[e].valid && key < kmax;
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s[e]), srsrc,
+                                                    st ? int(soff[e] + uint32_t(key) * 4u) : int(0x80000000u), 0, 0);
+            }
+            mx[e] = fmaxf(mx[e], s[e]);
           }
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], s[e]);
-      };
-      for (int t = my_lo; t < my_hi; t += 2) {
-        step(t, kA, kB);
-        if (t + 1 < my_hi) step(t + 1, kB, kA);
       }
     }
 #pragma unroll
@@ -366,135 +408,146 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 
   constexpr bool from_cache = MODE == ACCCACHED;
   // V chunk c = i*256 + tid of a tile: key c / VCH, d chunk (c % VCH) * CH
+  // (each wave instruction reads whole 16-byte-aligned key rows).
   auto v_entries = [&](int t, int (&ve)[VITER]) {
 #pragma unroll
-    for (int i = 0; i < VITER; ++i) ve[i] = bt_entry(clamp_key(t * TILE + (i * kThreads + tid) / VCH));
+    for (int i = 0; i < VITER; ++i)
+      ve[i] = bt_entry(clamp_key(t * TILE + (i * kThreads + tid) / VCH));
   };
-  auto v_load = [&](int t, const int (&ve)[VITER], uint4 (&vr)[VITER]) {
+  auto v_load = [&](int t, const int (&ve)[VITER], u32x4 (&vr)[VITER]) {
 #pragma unroll
     for (int i = 0; i < VITER; ++i) {
       const int c = i * kThreads + tid;
       const int key = clamp_key(t * TILE + c / VCH), d0 = (c % VCH) * CH;
-      vr[i] = d0 < a.head_dim ? *reinterpret_cast<const uint4*>(Vc + row_addr(key, ve[i], a.sv_b, a.sv_s, a.sv_h) + d0)
-                              : make_uint4(0, 0, 0, 0);
+      // columns past head_dim (read from column 0) only reach output
+      // columns that are never stored
+      vr[i] = *reinterpret_cast<const u32x4*>(Vc + row_addr(key, ve[i], a.sv_b, a.sv_s, a.sv_h) +
+                                              (d0 < a.head_dim ? d0 : 0));
     }
   };
   auto s_load = [&](int t, float (&s)[4]) {
     const int key = t * TILE + wave * 16 + (lane & 15);
+    const int64_t kc = key < a.lmax ? key : a.lmax - 1;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      s[e] = (srow[e].valid && key >= srow[e].kstart && key < srow[e].kend && key < a.lmax) ? *sc_addr(e, key)
-                                                                                         : -__builtin_inff();
+    for (int e = 0; e < 4; ++e) {
+      const float x = sbase[e][kc];
+      s[e] = (srow[e].valid && key >= srow[e].kstart && key < srow[e].kend && key < a.lmax) ? x
+                                                                                           : -__builtin_inff();
+    }
+  };
+
+  // One key tile: weights from the scores, V tile to LDS, PV partials.
+  auto accumulate = [&](int t, const u32x4 (&vr)[VITER], const float (&s)[4]) __attribute__((always_inline)) {
+    const int kin = wave * 16 + (lane & 15);  // key within the tile
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float w = __builtin_amdgcn_exp2f(s[e] - m[e]);
+      den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
+      Ps[(4 * kg + e) * VP + kin] = Io<DT>::store(w);
+    }
+#pragma unroll
+    for (int i = 0; i < VITER; ++i) {  // V tile -> LDS
+      const int c = i * kThreads + tid;
+      const int kk = c / VCH, d0 = (c % VCH) * CH;
+      if constexpr (TR16) {
+        *reinterpret_cast<u32x4*>(&Vt[kk * VNP + d0]) = vr[i];
+      } else {  // transposed to [d][key]
+        union {
+          u32x4 v;
+          T e[CH];
+        } u;
+        u.v = vr[i];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) Vt[(d0 + j) * VP + vcol(d0 + j, kk)] = u.e[j];
+      }
+    }
+    __syncthreads();
+    // PV: wave handles d blocks wave, wave+4, ...; one quantised chain per
+    // QUNIT keys
+#pragma unroll
+    for (int b = 0; b < DB_PER_WAVE; ++b) {
+      const int db = wave + 4 * b;
+      if (db < DBLK) {
+        const int dv = db * 16 + (lane & 15);
+#pragma unroll
+        for (int u0 = 0; u0 < TILE; u0 += QUNIT) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k0 = 0; k0 < QUNIT; k0 += KI) {
+            if constexpr (DT == FXPR_DTYPE_F32) {
+              const int key = u0 + k0 + kg;
+              acc = TR::mma(Ps[(lane & 15) * VP + key], Vt[dv * VP + vcol(dv, key)], acc);
+            } else {
+              // B operand: lane (kg, i) needs V[keys key..key+7][d = db*16 + i].
+              // ds_read_b64_tr_b16 gives lane i of each 16-lane group
+              // element (i % 4) of source lane 4c' + i/4, c' = 0..3; source
+              // lane j points at V[key0 + j/4][db*16 + 4*(j%4)].
+              const int key = u0 + k0 + 8 * kg;
+              const int j = lane & 15;
+              typedef short v4s __attribute__((ext_vector_type(4)));
+              const T* src = &Vt[(key + (j >> 2)) * VNP + db * 16 + 4 * (j & 3)];
+              const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(src));
+              const v4s hi4 =
+                  __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(src + 4 * VNP));
+              struct {
+                v4s a, b;
+              } both = {lo4, hi4};
+              acc = TR::mma(*reinterpret_cast<const u32x4*>(&Ps[(lane & 15) * VP + key]),
+                            __builtin_bit_cast(u32x4, both), acc);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+        }
+      }
+    }
+    __syncthreads();
   };
 
   if (my_lo < my_hi) {
-    // Ping-pong buffers, unrolled by two (see pass 1): V chunks, their page
-    // entries (fetched two tiles ahead), and K fragments or cached scores.
-    int veA[VITER], veB[VITER];
-    uint4 vrA[VITER], vrB[VITER];
-    KFrag kA[QSTEPS], kB[QSTEPS];
-    float scA[4], scB[4];
-    int ke_next = 0;
-    v_entries(my_lo, veA);
-    v_load(my_lo, veA, vrA);
-    v_entries(min(my_lo + 1, my_hi - 1), veB);
-    if constexpr (from_cache) {
-      s_load(my_lo, scA);
-    } else {
-      k_load(my_lo, k_entry(my_lo), kA);
-      ke_next = k_entry(min(my_lo + 1, my_hi - 1));
+    // Ring of R2 slots (V chunks and their page entries, plus the cached
+    // scores or the K fragments and their entries), scheduled as the pass-1
+    // ring: entries R2 steps ahead of their loads, compile-time slots.
+    constexpr int R2 = MODE == ACCCACHED ? 3 : 2;
+    u32x4 vb[R2][VITER];
+    int veb[R2][VITER];
+    float sb[R2][4];
+    KFrag kb[R2][QSTEPS];
+    int keb[R2];
+    auto tl = [&](int x) { return min(x, my_hi - 1); };
+    auto entries = [&](int x, int (&ve)[VITER], int& ke) {
+      v_entries(tl(x), ve);
+      if constexpr (!from_cache) ke = k_entry(tl(x));
+    };
+    auto loads = [&](int x, const int (&ve)[VITER], u32x4 (&vr)[VITER], float (&sc)[4], int ke,
+                     KFrag (&kf)[QSTEPS]) {
+      v_load(tl(x), ve, vr);
+      if constexpr (from_cache) s_load(tl(x), sc);
+      else k_load(tl(x), ke, kf);
+    };
+#pragma unroll
+    for (int i = 0; i < R2; ++i) entries(my_lo + i, veb[i], keb[i]);
+#pragma unroll
+    for (int i = 0; i + 1 < R2; ++i) {
+      loads(my_lo + i, veb[i], vb[i], sb[i], keb[i], kb[i]);
+      entries(my_lo + R2 + i, veb[i], keb[i]);
     }
-    // ve_nxt holds the entries of tile t + 1 on entry; refilled with t + 3's
-    // entries... entries of tile t + 2 go to ve_cur's array once its tile is
-    // loaded.
-    auto step = [&](int t, const uint4 (&vr_cur)[VITER], uint4 (&vr_nxt)[VITER], int (&ve_cur)[VITER],
-                    const int (&ve_nxt)[VITER], const KFrag (&kcur)[QSTEPS], KFrag (&knxt)[QSTEPS],
-                    const float (&sc_cur)[4], float (&sc_nxt)[4]) {
-      if (t + 1 < my_hi) {
-        v_load(t + 1, ve_nxt, vr_nxt);
-        if constexpr (from_cache) s_load(t + 1, sc_nxt);
-        else k_load(t + 1, ke_next, knxt);
-      }
-      v_entries(min(t + 2, my_hi - 1), ve_cur);  // ve_cur's tile is loaded: reuse it for t + 2
-      if constexpr (!from_cache) ke_next = k_entry(min(t + 2, my_hi - 1));
-
-      float s[4];
-      if constexpr (from_cache) {
+    for (int t = my_lo; t < my_hi; t += R2) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s[e] = sc_cur[e];
-      } else {
-        k_scores(t, kcur, s);
-      }
-      const int kin = wave * 16 + (lane & 15);  // key within the tile
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float w = __builtin_amdgcn_exp2f(s[e] - m[e]);
-        den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
-        Ps[(4 * kg + e) * VP + kin] = Io<DT>::store(w);
-      }
-#pragma unroll
-      for (int i = 0; i < VITER; ++i) {  // V tile -> LDS
-        const int c = i * kThreads + tid;
-        const int kk = c / VCH, d0 = (c % VCH) * CH;
-        if constexpr (TR16) {
-          *reinterpret_cast<uint4*>(&Vt[kk * VNP + d0]) = vr_cur[i];
-        } else {  // transposed to [d][key]
-          union {
-            uint4 v;
-            T e[CH];
-          } u;
-          u.v = vr_cur[i];
-#pragma unroll
-          for (int j = 0; j < CH; ++j) Vt[(d0 + j) * VP + vcol(d0 + j, kk)] = u.e[j];
-        }
-      }
-      __syncthreads();
-      // PV: wave handles d blocks wave, wave+4, ...; one quantised chain per
-      // QUNIT keys
-#pragma unroll
-      for (int b = 0; b < DB_PER_WAVE; ++b) {
-        const int db = wave + 4 * b;
-        if (db < DBLK) {
-          const int dv = db * 16 + (lane & 15);
-#pragma unroll
-          for (int u0 = 0; u0 < TILE; u0 += QUNIT) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int k0 = 0; k0 < QUNIT; k0 += KI) {
-              if constexpr (DT == FXPR_DTYPE_F32) {
-                const int key = u0 + k0 + kg;
-                acc = TR::mma(Ps[(lane & 15) * VP + key], Vt[dv * VP + vcol(dv, key)], acc);
-              } else {
-                // B operand: lane (kg, i) needs V[keys key..key+7][d = db*16 + i].
-                // ds_read_b64_tr_b16 gives lane i of each 16-lane group
-                // element (i % 4) of source lane 4c' + i/4, c' = 0..3; source
-                // lane j points at V[key0 + j/4][db*16 + 4*(j%4)].
-                const int key = u0 + k0 + 8 * kg;
-                const int j = lane & 15;
-                typedef short v4s __attribute__((ext_vector_type(4)));
-                const T* src = &Vt[(key + (j >> 2)) * VNP + db * 16 + 4 * (j & 3)];
-                const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) v4s*)(src));
-                const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) v4s*)(src + 4 * VNP));
-                struct {
-                  v4s a, b;
-                } both = {lo4, hi4};
-                acc = TR::mma(*reinterpret_cast<const uint4*>(&Ps[(lane & 15) * VP + key]),
-                              __builtin_bit_cast(uint4, both), acc);
-              }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+      for (int u = 0; u < R2; ++u) {
+        const int sl = (u + R2 - 1) % R2;
+        loads(t + u + R2 - 1, veb[sl], vb[sl], sb[sl], keb[sl], kb[sl]);
+        entries(t + u + 2 * R2 - 1, veb[sl], keb[sl]);
+        if (t + u < my_hi) {
+          if constexpr (from_cache) {
+            accumulate(t + u, vb[u], sb[u]);
+          } else {
+            float s[4];
+            k_scores(t + u, kb[u], s);
+            accumulate(t + u, vb[u], s);
           }
         }
       }
-      __syncthreads();
-    };
-    for (int t = my_lo; t < my_hi; t += 2) {
-      step(t, vrA, vrB, veA, veB, kA, kB, scA, scB);
-      if (t + 1 < my_hi) step(t + 1, vrB, vrA, veB, veA, kB, kA, scB, scA);
     }
   }
 
