@@ -66,6 +66,7 @@ extern "C" int fxpr_gemm(const void* a, const void* b, const float* bias, void* 
   args.inv_scale = pow2f(-frac_bits);
   args.ktiles = int(cdiv(k, ktile_for(io_dtype)));
   args.tiles_per_split = int(cdiv(args.ktiles, splits));
+  args.c_vec = (stride_cn == 1 || n == 1) && stride_cm % ch == 0 && aligned(c, 16);
   hipStream_t st = as_stream(stream);
 
   switch (io_dtype) {

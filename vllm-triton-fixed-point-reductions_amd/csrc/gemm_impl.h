@@ -25,6 +25,7 @@ namespace gemm {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;  // 4 waves per workgroup
 
@@ -77,6 +78,7 @@ struct GemmArgs {
   int64_t scm, scn;  // C strides
   float scale, inv_scale;
   int ktiles, tiles_per_split, tiles_m, tiles_n;
+  int c_vec;         // C rows unit-stride, 16-byte aligned (vector row stores)
 };
 
 template <int BITS> struct Acc { using T = int32_t; };
@@ -360,6 +362,299 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, 
 }
 
 // ---------------------------------------------------------------------------
+// Large-M kernel for 16-bit inputs with K-contiguous A and B (the lm_head /
+// linear layout). Same per-output MFMA chain as gemm_fxp_kernel (16x16x32,
+// increasing k, zero C at each 128-wide K-tile), so results are bitwise
+// identical to every other configuration; only the schedule differs.
+//
+// 8 waves (two per SIMD) over a 256 x 128 workgroup tile, 64 x 64 per wave.
+// A and B stages (64 k) go straight from global memory into LDS with
+// global_load_lds_dwordx4 (no staging registers), three stages in flight.
+// Rows are 128 B with the 16-byte chunk c of row r stored at slot
+// c ^ ((r >> 1) & 7): each DMA instruction fills 1 KB of LDS contiguously,
+// and the 16-row fragment reads hit 16 distinct 16-byte bank groups.
+// The compiler would wait for every outstanding DMA before any LDS read it
+// can see, so fragment reads are inline asm and the waits are explicit: the
+// DMAs of stage s are complete once only the next stage's are outstanding
+// (vector memory operations complete in issue order), and a barrier makes
+// every wave's part visible. A partial last K-tile is peeled off and done
+// first (integer sums do not depend on the order of tiles). The epilogue
+// stages each wave's C tile through LDS to write whole 16-byte row pieces.
+
+template <int BM_, int BN_, int WGM_, int WGN_> struct BigTile {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+  static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
+  static constexpr int MB = WM / 16, NB = WN / 16;
+};
+using TB = BigTile<256, 128, 4, 2>;
+constexpr int kBigStages = 3;
+
+template <class BT> constexpr size_t big_lds_bytes() {
+  constexpr size_t stages = size_t(kBigStages) * (BT::BM + BT::BN) * 128;
+  constexpr size_t epi = size_t(BT::WAVES) * BT::WM * (BT::WN + 8) * 2;
+  return stages > epi ? stages : epi;
+}
+
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+template <int DT, int BITS, class BT, bool SPLIT>
+__global__ __launch_bounds__(BT::THREADS) void gemm_big_kernel(GemmArgs args) {
+  using M_ = Mma<DT>;
+  using T = typename M_::T;
+  using AccT = typename Acc<BITS>::T;
+  static_assert(DT != FXPR_DTYPE_F32, "16-bit inputs only");
+  static_assert(BT::MB == 4 && BT::NB == 4, "fragment asm assumes 64 x 64 wave tiles");
+  constexpr int BM = BT::BM, BN = BT::BN, MB = BT::MB, NB = BT::NB, NW = BT::WAVES;
+  constexpr int BKS = 64, CH = 8;
+  constexpr int STAGE = (BM + BN) * 128;  // bytes per LDS stage
+  constexpr int NIA = BM / 8 / NW;        // A DMA instructions per wave per stage (8 rows each)
+  constexpr int NIB = BN / 8 / NW;        // B DMA instructions per wave per stage
+  constexpr int NDMA = NIA + NIB;         // vector memory instructions per wave per stage
+  static_assert(NIA * 8 * NW == BM && NIB * 8 * NW == BN, "tile / wave mismatch");
+
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(smem_raw));
+
+  const T* A = static_cast<const T*>(args.a);
+  const T* B = static_cast<const T*>(args.b);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / BT::WGN, wn = wave % BT::WGN;
+  int tm, tn;
+  tile_coords(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, tm, tn);
+  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+  const int split = blockIdx.y;
+  const int kt_begin = split * args.tiles_per_split;
+  const int kt_end = min(args.ktiles, kt_begin + args.tiles_per_split);
+  const bool has_tail = kt_end > kt_begin && int64_t(kt_end) * 128 > args.K;
+  const int nfull = max(0, kt_end - kt_begin - (has_tail ? 1 : 0));
+  const int64_t kb0 = int64_t(kt_begin) * 128;
+
+  // DMA sources. Instruction q of this wave covers rows 8 i .. 8 i + 7 of
+  // the A (B) stage, i = wave + NW q; lane l brings row 8 i + l / 8, chunk
+  // (l % 8) ^ ((row >> 1) & 7). Rows past M / N are clamped: they feed only
+  // outputs that are never stored.
+  const T* src[NDMA];
+#pragma unroll
+  for (int q = 0; q < NDMA; ++q) {
+    const bool isa = q < NIA;
+    const int i = wave + NW * (isa ? q : q - NIA);
+    const int r = 8 * i + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    if (isa) {
+      const int64_t m = min<int64_t>(m0 + r, args.M - 1);
+      src[q] = A + m * args.lda + kb0 + c * CH;
+    } else {
+      const int64_t n = min<int64_t>(n0 + r, args.N - 1);
+      src[q] = B + n * args.ldb + kb0 + c * CH;
+    }
+  }
+  auto dma = [&](int s, int buf) {  // stage s (64 k from kb0) into LDS buffer buf
+#pragma unroll
+    for (int q = 0; q < NDMA; ++q) {
+      const bool isa = q < NIA;
+      const int i = wave + NW * (isa ? q : q - NIA);
+      const unsigned dst = lds0 + buf * STAGE + (isa ? 0 : BM * 128) + i * 1024;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src[q] + int64_t(s) * BKS),
+                                       (LdsPtr)(uintptr_t)dst, 16, 0, 0);
+    }
+  };
+
+  f32x4 P[MB][NB];
+  AccT I[MB][NB][4];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) I[i][j][r] = 0;
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+
+  // Fragment reads: lane (row lane % 16 of each 16-row block, k slot kg)
+  // reads chunk c = 4 h + kg of its row; the row's swizzle (row >> 1) & 7
+  // depends on lane % 16 only (blocks start at multiples of 16).
+  const int kg = lane >> 4, sw = (lane & 15) >> 1;
+  const unsigned arow = (wm * BT::WM + (lane & 15)) * 128;
+  const unsigned brow = BM * 128 + (wn * BT::WN + (lane & 15)) * 128;
+  auto frags = [&](int buf, int h, u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
+    const unsigned off = lds0 + buf * STAGE + ((((h << 2) + kg) ^ sw) << 4);
+    const unsigned aa = off + arow, bb = off + brow;
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:2048\n\t"
+        "ds_read_b128 %2, %8 offset:4096\n\t"
+        "ds_read_b128 %3, %8 offset:6144\n\t"
+        "ds_read_b128 %4, %9\n\t"
+        "ds_read_b128 %5, %9 offset:2048\n\t"
+        "ds_read_b128 %6, %9 offset:4096\n\t"
+        "ds_read_b128 %7, %9 offset:6144"
+        : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fb[0]), "=&v"(fb[1]), "=&v"(fb[2]),
+          "=&v"(fb[3])
+        : "v"(aa), "v"(bb)
+        : "memory");
+  };
+  auto lds_wait = [&](u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]), "+v"(fb[2]),
+                   "+v"(fb[3])
+                 :
+                 : "memory");
+  };
+  auto mfmas = [&](const u32x4 (&fa)[MB], const u32x4 (&fb)[NB], bool zero_c) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        P[i][j] = M_::mma(__builtin_bit_cast(uint4, fa[i]), __builtin_bit_cast(uint4, fb[j]), zero_c ? zero4 : P[i][j]);
+  };
+  // One 64-k stage from LDS buffer buf: the h = 1 fragments load while the
+  // h = 0 MFMAs run.
+  auto compute = [&](int buf, bool first) {
+    u32x4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
+    frags(buf, 0, fa0, fb0);
+    lds_wait(fa0, fb0);
+    frags(buf, 1, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa0, fb0, first);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_wait(fa1, fb1);
+    mfmas(fa1, fb1, false);
+  };
+  auto quantize = [&]() {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) I[i][j][r] = wrap_add<BITS>(I[i][j][r], quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
+  };
+
+  // Partial last K-tile first: masked register loads (zero past K) written
+  // in the same swizzled layout, both stages.
+  if (has_tail) {
+    const int64_t kt0 = int64_t(kt_end - 1) * 128;
+    for (int e = tid; e < 2 * (BM + BN) * 8; e += BT::THREADS) {
+      const int st = e / ((BM + BN) * 8), rem = e % ((BM + BN) * 8);
+      const int r = rem / 8, c = rem % 8;
+      const int64_t k = kt0 + st * BKS + c * CH;
+      const bool isa = r < BM;
+      const int64_t row = isa ? m0 + r : n0 + (r - BM);
+      const bool ok = isa ? row < args.M : row < args.N;
+      const int valid = (ok && k < args.K) ? int(min<int64_t>(CH, args.K - k)) : 0;
+      const T* base = isa ? A + (valid ? row * args.lda + k : 0) : B + (valid ? row * args.ldb + k : 0);
+      const uint4 v = load_chunk<false>(base, valid);
+      const int rr = isa ? r : r - BM;
+      *reinterpret_cast<uint4*>(smem_raw + st * STAGE + (isa ? 0 : BM * 128) + rr * 128 +
+                                ((c ^ ((rr >> 1) & 7)) << 4)) = v;
+    }
+    __syncthreads();
+    compute(0, true);
+    compute(1, false);
+    quantize();
+    __syncthreads();
+  }
+
+  // Pipelined full K-tiles: stage s = 64 k in LDS buffer s % 3, DMAs two
+  // stages ahead. Stages past the end re-load the last one into the free
+  // buffer (never read), so every iteration issues the same DMAs and the
+  // wait count stays exact.
+  const int nst = 2 * nfull;
+  if (nst > 0) {
+    dma(0, 0);
+    dma(min(1, nst - 1), 1);
+    for (int s = 0; s < nst; ++s) {
+      const int buf = s % kBigStages;
+      // Own DMAs of stage s landed; the barrier then covers everyone's and
+      // frees buffer (s+2)%3 (its last reads finished in iteration s-1). A
+      // plain s_barrier: __syncthreads() would also fence, i.e. wait for
+      // every DMA in flight.
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
+      __builtin_amdgcn_s_barrier();
+      dma(min(s + 2, nst - 1), (s + 2) % kBigStages);
+      compute(buf, (s & 1) == 0);
+      if (s & 1) quantize();
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing DMAs into unused buffers
+  }
+  __syncthreads();  // LDS is reused by the epilogue
+
+  // Epilogue. Lane holds rows 4*(lane/16)+r of each 16x16 block, column lane%16.
+  const int64_t row_base = m0 + wm * BT::WM + kg * 4;
+  const int64_t col_base = n0 + wn * BT::WN + (lane & 15);
+  if constexpr (SPLIT) {
+    AccT* ws = static_cast<AccT*>(args.ws) + int64_t(split) * args.M * args.N;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int64_t n = col_base + j * 16;
+        if (n >= args.N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = row_base + i * 16 + r;
+          if (m < args.M) ws[m * args.N + n] = I[i][j][r];
+        }
+      }
+  } else {
+    T* C = static_cast<T*>(args.c);
+    const float* bias = args.bias;
+    float bv[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int64_t n = col_base + j * 16;
+      bv[j] = (bias && n < args.N) ? bias[n] : 0.0f;
+    }
+    auto value = [&](int i, int j, int r) {
+      float v = acc_to_f32<BITS>(I[i][j][r], args.inv_scale);
+      if (bias) v = __fadd_rn(v, bv[j]);
+      return Io<DT>::store(v);
+    };
+    if (args.c_vec) {
+      // wave tile -> LDS (wave-private [WM][WN + 8]) -> 16-byte row stores
+      constexpr int EP = BT::WN + 8;
+      T* ep = reinterpret_cast<T*>(smem_raw) + wave * BT::WM * EP;
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ep[(i * 16 + kg * 4 + r) * EP + j * 16 + (lane & 15)] = value(i, j, r);
+      __builtin_amdgcn_wave_barrier();
+      constexpr int CPR = BT::WN / CH;  // 16-byte chunks per row
+#pragma unroll
+      for (int it = 0; it < BT::WM * CPR / 64; ++it) {
+        const int c = it * 64 + lane;
+        const int row = c / CPR, col = (c % CPR) * CH;
+        const int64_t m = m0 + wm * BT::WM + row, n = n0 + wn * BT::WN + col;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ep + row * EP + col);
+        if (m < args.M) {
+          if (n + CH <= args.N) {
+            *reinterpret_cast<u32x4*>(C + m * args.scm + n) = v;
+          } else {
+            const T* e = reinterpret_cast<const T*>(&v);
+            for (int q = 0; q < CH; ++q)
+              if (n + q < args.N) C[m * args.scm + n + q] = e[q];
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int64_t n = col_base + j * 16;
+        if (n >= args.N) continue;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t m = row_base + i * 16 + r;
+            if (m < args.M) C[m * args.scm + n * args.scn] = value(i, j, r);
+          }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 
 template <int DT, class TL> constexpr size_t lds_bytes() {
@@ -380,6 +675,26 @@ int launch_tile(const GemmArgs& a, int splits, hipStream_t st) {
   dim3 grid(unsigned(a.tiles_m * a.tiles_n), unsigned(splits));
   kern<<<grid, kThreads, lds, st>>>(a);
   return launch_status();
+}
+
+template <int DT, int BITS, class BT>
+int launch_big(GemmArgs a, int splits, hipStream_t st) {
+  a.tiles_m = int(cdiv(a.M, BT::BM));
+  a.tiles_n = int(cdiv(a.N, BT::BN));
+  constexpr size_t lds = big_lds_bytes<BT>();
+  auto go = [&](auto kern) -> int {
+    static bool attr_done = false;  // benign race: the attribute is idempotent
+    if (!attr_done) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+      if (e != hipSuccess) return int(e);
+      attr_done = true;
+    }
+    kern<<<dim3(unsigned(a.tiles_m * a.tiles_n), unsigned(splits)), BT::THREADS, lds, st>>>(a);
+    return launch_status();
+  };
+  if (splits > 1) return go(gemm_big_kernel<DT, BITS, BT, true>);
+  return go(gemm_big_kernel<DT, BITS, BT, false>);
 }
 
 template <int DT, int BITS, class TL, bool BNC, bool VEC>
@@ -420,6 +735,9 @@ inline void tile_dims(TileId t, int& bm, int& bn) {
 template <int DT, int BITS>
 int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
   const TileId t = pick_tile(a.M);
+  if constexpr (DT != FXPR_DTYPE_F32 && BITS != 64) {
+    if (vec && !b_ncontig && t == TileId::Big) return launch_big<DT, BITS, TB>(a, splits, st);
+  }
   if (vec && !b_ncontig) {
     switch (t) {
       case TileId::M16: return launch_cfg<DT, BITS, T16, false, true>(a, splits, st);
@@ -458,6 +776,10 @@ inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int req
   } else {
     int bm, bn;
     tile_dims(pick_tile(M), bm, bn);
+    if (pick_tile(M) == TileId::Big && io_dtype != FXPR_DTYPE_F32) {
+      bm = TB::BM;
+      bn = TB::BN;
+    }
     const int64_t tiles = cdiv(M, bm) * cdiv(N, bn);
     if (tiles >= 256) return 1;
     s = int(512 / tiles);
