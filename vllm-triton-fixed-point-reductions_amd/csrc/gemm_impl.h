@@ -16,6 +16,8 @@
 
 #pragma once
 
+#include <type_traits>
+
 #include "fxp_device.h"
 #include "fxpr_internal.h"
 
@@ -472,26 +474,28 @@ __global__ __launch_bounds__(BT::THREADS) void gemm_big_kernel(GemmArgs args) {
 
   // Fragment reads: lane (row lane % 16 of each 16-row block, k slot kg)
   // reads chunk c = 4 h + kg of its row; the row's swizzle (row >> 1) & 7
-  // depends on lane % 16 only (blocks start at multiples of 16).
+  // depends on lane % 16 only (blocks start at multiples of 16). Fragment
+  // f < 4 is A block f, f >= 4 is B block f - 4 (16 rows = 2048 B apart).
   const int kg = lane >> 4, sw = (lane & 15) >> 1;
   const unsigned arow = (wm * BT::WM + (lane & 15)) * 128;
   const unsigned brow = BM * 128 + (wn * BT::WN + (lane & 15)) * 128;
-  auto frags = [&](int buf, int h, u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
-    const unsigned off = lds0 + buf * STAGE + ((((h << 2) + kg) ^ sw) << 4);
-    const unsigned aa = off + arow, bb = off + brow;
-    asm volatile(
-        "ds_read_b128 %0, %8\n\t"
-        "ds_read_b128 %1, %8 offset:2048\n\t"
-        "ds_read_b128 %2, %8 offset:4096\n\t"
-        "ds_read_b128 %3, %8 offset:6144\n\t"
-        "ds_read_b128 %4, %9\n\t"
-        "ds_read_b128 %5, %9 offset:2048\n\t"
-        "ds_read_b128 %6, %9 offset:4096\n\t"
-        "ds_read_b128 %7, %9 offset:6144"
-        : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fb[0]), "=&v"(fb[1]), "=&v"(fb[2]),
-          "=&v"(fb[3])
-        : "v"(aa), "v"(bb)
-        : "memory");
+  auto frag_addr = [&](int buf, int h, bool isb) -> unsigned {
+    return lds0 + buf * STAGE + ((((h << 2) + kg) ^ sw) << 4) + (isb ? brow : arow);
+  };
+  auto read_frag = [&](unsigned addr, u32x4& x, auto off_tag) {
+    constexpr int OFF = decltype(off_tag)::value;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(x) : "v"(addr), "n"(OFF) : "memory");
+  };
+  auto read_frags = [&](int buf, int h, u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
+    const unsigned aa = frag_addr(buf, h, false), bb = frag_addr(buf, h, true);
+    read_frag(aa, fa[0], std::integral_constant<int, 0>{});
+    read_frag(aa, fa[1], std::integral_constant<int, 2048>{});
+    read_frag(aa, fa[2], std::integral_constant<int, 4096>{});
+    read_frag(aa, fa[3], std::integral_constant<int, 6144>{});
+    read_frag(bb, fb[0], std::integral_constant<int, 0>{});
+    read_frag(bb, fb[1], std::integral_constant<int, 2048>{});
+    read_frag(bb, fb[2], std::integral_constant<int, 4096>{});
+    read_frag(bb, fb[3], std::integral_constant<int, 6144>{});
   };
   auto lds_wait = [&](u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
     asm volatile("s_waitcnt lgkmcnt(0)"
@@ -500,34 +504,41 @@ __global__ __launch_bounds__(BT::THREADS) void gemm_big_kernel(GemmArgs args) {
                  :
                  : "memory");
   };
-  auto mfmas = [&](const u32x4 (&fa)[MB], const u32x4 (&fb)[NB], bool zero_c) {
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-        P[i][j] = M_::mma(__builtin_bit_cast(uint4, fa[i]), __builtin_bit_cast(uint4, fb[j]), zero_c ? zero4 : P[i][j]);
+  auto mma = [&](int i, int j, const u32x4& a, const u32x4& b, bool zero_c) {
+    P[i][j] = M_::mma(__builtin_bit_cast(uint4, a), __builtin_bit_cast(uint4, b), zero_c ? zero4 : P[i][j]);
   };
-  // One 64-k stage from LDS buffer buf: the h = 1 fragments load while the
-  // h = 0 MFMAs run.
-  auto compute = [&](int buf, bool first) {
-    u32x4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
-    frags(buf, 0, fa0, fb0);
-    lds_wait(fa0, fb0);
-    frags(buf, 1, fa1, fb1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(fa0, fb0, first);
-    __builtin_amdgcn_sched_barrier(0);
-    lds_wait(fa1, fb1);
-    mfmas(fa1, fb1, false);
+  auto quantize_block = [&](int i, int j) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) I[i][j][r] = wrap_add<BITS>(I[i][j][r], quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
   };
   auto quantize = [&]() {
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) I[i][j][r] = wrap_add<BITS>(I[i][j][r], quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
+      for (int j = 0; j < NB; ++j) quantize_block(i, j);
   };
+  // Plain (unpipelined) stage, used for the peeled tail tile.
+  auto compute = [&](int buf, bool first) {
+    u32x4 fa[MB], fb[NB];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      read_frags(buf, h, fa, fb);
+      lds_wait(fa, fb);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) mma(i, j, fa[i], fb[j], first && h == 0);
+    }
+  };
+
+  // P holds the fp32 partial of the K-tile in progress; it is quantised into
+  // I when the next K-tile starts (block by block, in the shadow of the new
+  // chain's MFMAs) and once more after the last one. Starting from zero,
+  // the first such quantisation adds nothing.
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) P[i][j] = zero4;
 
   // Partial last K-tile first: masked register loads (zero past K) written
   // in the same swizzled layout, both stages.
@@ -550,32 +561,71 @@ __global__ __launch_bounds__(BT::THREADS) void gemm_big_kernel(GemmArgs args) {
     __syncthreads();
     compute(0, true);
     compute(1, false);
-    quantize();
     __syncthreads();
   }
 
   // Pipelined full K-tiles: stage s = 64 k in LDS buffer s % 3, DMAs two
   // stages ahead. Stages past the end re-load the last one into the free
   // buffer (never read), so every iteration issues the same DMAs and the
-  // wait count stays exact.
+  // wait count stays exact. Per stage: issue DMAs; the h = 0 MFMAs (with the
+  // previous K-tile's quantisation interleaved at a K-tile start, and the
+  // h = 1 fragment reads issued between them); the h = 1 MFMAs; wait for the
+  // next stage's DMAs and barrier; issue the next stage's h = 0 fragment
+  // reads, which complete while the MFMAs drain.
   const int nst = 2 * nfull;
   if (nst > 0) {
+    u32x4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
     dma(0, 0);
     dma(min(1, nst - 1), 1);
-    for (int s = 0; s < nst; ++s) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
+    __builtin_amdgcn_s_barrier();
+    read_frags(0, 0, fa0, fb0);
+    auto stage = [&](int s, bool tile_start) {
       const int buf = s % kBigStages;
-      // Own DMAs of stage s landed; the barrier then covers everyone's and
-      // frees buffer (s+2)%3 (its last reads finished in iteration s-1). A
-      // plain s_barrier: __syncthreads() would also fence, i.e. wait for
-      // every DMA in flight.
+      dma(min(s + 2, nst - 1), (s + 2) % kBigStages);
+      lds_wait(fa0, fb0);
+      const unsigned aa1 = frag_addr(buf, 1, false), bb1 = frag_addr(buf, 1, true);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < MB * NB; ++b) {
+        const int i = b / NB, j = b % NB;
+        if (tile_start) quantize_block(i, j);
+        mma(i, j, fa0[i], fb0[j], tile_start);
+        switch (b) {
+          case 0: read_frag(aa1, fa1[0], std::integral_constant<int, 0>{}); break;
+          case 2: read_frag(aa1, fa1[1], std::integral_constant<int, 2048>{}); break;
+          case 4: read_frag(aa1, fa1[2], std::integral_constant<int, 4096>{}); break;
+          case 6: read_frag(aa1, fa1[3], std::integral_constant<int, 6144>{}); break;
+          case 8: read_frag(bb1, fb1[0], std::integral_constant<int, 0>{}); break;
+          case 10: read_frag(bb1, fb1[1], std::integral_constant<int, 2048>{}); break;
+          case 12: read_frag(bb1, fb1[2], std::integral_constant<int, 4096>{}); break;
+          case 14: read_frag(bb1, fb1[3], std::integral_constant<int, 6144>{}); break;
+          default: break;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      lds_wait(fa1, fb1);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) mma(i, j, fa1[i], fb1[j], false);
+      __builtin_amdgcn_sched_barrier(0);
+      // Own DMAs of stage s + 1 landed; the barrier covers everyone's, and
+      // everyone's reads of stage s are done (buffer s % 3 is refilled two
+      // stages later). A plain s_barrier: __syncthreads() would also fence,
+      // i.e. wait for the DMAs of stage s + 2 as well.
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
       __builtin_amdgcn_s_barrier();
-      dma(min(s + 2, nst - 1), (s + 2) % kBigStages);
-      compute(buf, (s & 1) == 0);
-      if (s & 1) quantize();
+      read_frags((s + 1) % kBigStages, 0, fa0, fb0);
+    };
+    for (int s = 0; s < nst; s += 2) {
+      stage(s, true);
+      stage(s + 1, false);
     }
+    lds_wait(fa0, fb0);                               // trailing reads (unused)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing DMAs into unused buffers
   }
+  quantize();
   __syncthreads();  // LDS is reused by the epilogue
 
   // Epilogue. Lane holds rows 4*(lane/16)+r of each 16x16 block, column lane%16.
