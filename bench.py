@@ -86,6 +86,22 @@ def hbm_roofline(bytes_per_call: float, ms: float) -> dict:
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
 
 
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the workload's dominant kernel, from the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs summarised in
+    profiles/hbm_traffic.md (counter KiB scaled by the factor a plain copy of
+    known size reads), or None when the workload was not profiled."""
+    path = ROOT / "profiles" / "hbm_traffic.md"
+    try:
+        for line in path.read_text().splitlines():
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 5 and cells[0] == f"`{workload}`":
+                return int(cells[-1].replace(",", ""))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def mfma_roofline(flops: float, ms: float, peak: float = BF16_PEAK_TFLOPS) -> dict:
     tf = flops / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
@@ -237,6 +253,18 @@ def wl_decode(steps, warmup, splits=0, int_bits=32, frac_bits=16, B=64, hq=32, h
             "ms": round(ms, 5), "bytes": nbytes, "splits": s_eff, "roofline": hbm_roofline(nbytes, ms)}
 
 
+def wl_hbm_copy(steps, warmup, nbytes=1 << 30):
+    """torch copy_ of a known size: the reference point for HBM bandwidth and
+    for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    src = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    ms = time_op(lambda: dst.copy_(src), [()], steps, warmup)
+    return {"workload": f"torch copy_ {nbytes} B", "ms": round(ms, 5), "bytes": 2 * nbytes,
+            "roofline": hbm_roofline(2 * nbytes, ms)}
+
+
 WORKLOADS = {
     "decode_attn": lambda s, w: wl_decode(s, w, 0),
     "decode_attn_s1": lambda s, w: wl_decode(s, w, 1),
@@ -256,6 +284,7 @@ WORKLOADS = {
     "rms_norm_q32i64": lambda s, w: wl_rms_norm(s, w, 64, 32),
     "log_softmax": lambda s, w: wl_log_softmax(s, w, 32, 16),
     "log_softmax_f32out_q32i64": lambda s, w: wl_log_softmax(s, w, 64, 32, fp32_out=True),
+    "hbm_copy": lambda s, w: wl_hbm_copy(s, w),
 }
 HEADLINE_ORDER = ["gemm_lm_head", "decode_attn", "rms_norm"]
 
@@ -343,6 +372,7 @@ def main() -> None:
     for name in names:
         log(f"workload {name} ...")
         results[name] = WORKLOADS[name](args.steps, args.warmup)
+        results[name]["roofline"]["traffic"] = measured_traffic(name)
         log(f"  {json.dumps(results[name])}")
 
     headline = next((h for h in HEADLINE_ORDER if h in results), names[0])

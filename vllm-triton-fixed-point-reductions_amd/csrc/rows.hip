@@ -16,7 +16,15 @@
 namespace fxpr {
 namespace {
 
-template <typename T, int N> struct alignas(sizeof(T) * N) Vec { T v[N]; };
+// N consecutive elements. For N > 1 a native vector, so arrays of them stay
+// in registers (a struct holding a plain array is copied with memcpys that
+// keep such arrays in scratch memory).
+template <typename T, int N, bool = (N > 1)> struct VecImpl { T v[N]; };
+template <typename T, int N> struct alignas(sizeof(T) * N) VecImpl<T, N, true> {
+  typedef T VT __attribute__((ext_vector_type(N)));
+  VT v;
+};
+template <typename T, int N> using Vec = VecImpl<T, N>;
 
 constexpr int kMaxThreads = 1024;
 
@@ -47,9 +55,27 @@ __device__ uint64_t block_sat_sum(uint64_t v, uint64_t qmax, uint64_t* smem) {
   return r;
 }
 
+__device__ __forceinline__ uint32_t cvt_sat_u32(float integral) {
+  // v_cvt_u32_f32 saturates to [0, 2^32 - 1] and maps NaN to 0
+  uint32_t o;
+  asm("v_cvt_u32_f32 %0, %1" : "=v"(o) : "v"(integral));
+  return o;
+}
+
 template <int BITS> __device__ __forceinline__ uint64_t quant_nonneg(float s) {
   // s >= 0 or NaN, so the result is in [0, qmax]
-  return static_cast<uint64_t>(quant<BITS>(s));
+  if constexpr (BITS == 64) {
+    // RNE, then split r = h 2^32 + l exactly (r integral, h = floor(r 2^-32));
+    // branch-free, so arrays of row values around it stay in registers.
+    // NaN -> 0; r >= 2^63 -> qmax (the caller's saturating add needs b <= qmax).
+    const float r = __builtin_rintf(s);
+    const float h = __builtin_floorf(__fmul_rn(r, 2.3283064365386963e-10f));
+    const float l = __fsub_rn(r, __fmul_rn(h, 4294967296.0f));
+    const uint64_t v = (static_cast<uint64_t>(cvt_sat_u32(h)) << 32) | cvt_sat_u32(l);
+    return v > 0x7fffffffffffffffull ? 0x7fffffffffffffffull : v;
+  } else {
+    return static_cast<uint64_t>(quant<BITS>(s));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -200,11 +226,11 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
   }
 }
 
-inline int threads_for(int64_t nchunks, int per_thread) {
+inline int threads_for(int64_t nchunks, int per_thread, int max_threads = kMaxThreads) {
   int64_t t = cdiv(nchunks, per_thread);
   t = cdiv(t, 64) * 64;
   if (t < 64) t = 64;
-  if (t > kMaxThreads) t = kMaxThreads;
+  if (t > max_threads) t = max_threads;
   return static_cast<int>(t);
 }
 
@@ -258,16 +284,21 @@ int launch_rms(const void* x, void* r, const void* w, void* y, int64_t rows, int
 // lse = m + ln(fl32(S) * 2^-f) (ln by log_own; S == 0 gives -inf).
 // Pass 3: y_j = OUT(fl32(x_j) - lse).
 
+// Log-softmax workgroups are at most 512 threads (two waves per SIMD), so a
+// thread may hold 256 registers: a 128256-wide bf16 row stays in registers
+// (32 x 16 bytes per thread) next to the exp / log temporaries, unspilled.
+constexpr int kLsmThreads = 512;
+
 template <int XDT, int YDT, int VEC, int NREG, int BITS>
-__global__ __launch_bounds__(kMaxThreads) void log_softmax_kernel(
+__global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
     const typename Io<XDT>::T* __restrict__ x, typename Io<YDT>::T* __restrict__ y, int64_t cols,
     int frac, float inv_scale, uint64_t qmax) {
   using XT = typename Io<XDT>::T;
   using YT = typename Io<YDT>::T;
   using XV = Vec<XT, VEC>;
   using YV = Vec<YT, VEC>;
-  __shared__ float fred[kMaxThreads / 64];
-  __shared__ uint64_t ired[kMaxThreads / 64];
+  __shared__ float fred[kLsmThreads / 64];
+  __shared__ uint64_t ired[kLsmThreads / 64];
 
   const int64_t row = blockIdx.x;
   const int64_t nchunks = cols / VEC;
@@ -333,9 +364,9 @@ int launch_lsm_vec(const void* x, void* y, int64_t rows, int64_t cols, int bits,
                    hipStream_t st) {
   using XT = typename Io<XDT>::T;
   using YT = typename Io<YDT>::T;
-  constexpr int NREG = VEC == 1 ? 8 : 16;
+  constexpr int NREG = VEC == 1 ? 8 : 32;
   const int64_t nchunks = cols / VEC;
-  const int nthr = threads_for(nchunks, NREG);
+  const int nthr = threads_for(nchunks, NREG, kLsmThreads);
   const float inv = pow2f(-frac);
   const uint64_t qmax = qmax_for_bits(bits);
   dim3 grid(static_cast<unsigned>(rows));
