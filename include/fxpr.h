@@ -192,6 +192,28 @@ int64_t fxpr_attention_workspace_bytes(int num_requests, int64_t num_tokens,
                                        int num_kv_splits, int max_query_len,
                                        int max_blocks_per_seq, int page_size);
 
+/*
+ * Paged KV-cache write: for each token t with slot = slot_mapping[t] >= 0,
+ * k_cache[slot / block_size, slot % block_size, h, :] = key[t, h, :] and the
+ * same for value / v_cache (the two halves of a vLLM [num_blocks, 2,
+ * block_size, num_kv_heads, head_size] cache). Negative slots (padding) and
+ * slots >= num_blocks * block_size are skipped. dtype: f16 / bf16 / f32 for
+ * all four tensors; head rows must be 16-byte aligned (strides in elements).
+ * A bit-exact copy.
+ * Replaces reshape_and_cache_flash as called by the reference backend's
+ * do_kv_cache_update (fxpr_vllm/attention_backend.py:253-277).
+ */
+int fxpr_reshape_and_cache(const void* key, const void* value, void* k_cache,
+                           void* v_cache, int dtype,
+                           const int64_t* slot_mapping, int64_t num_tokens,
+                           int num_kv_heads, int head_size, int block_size,
+                           int64_t num_blocks, int64_t stride_key_token,
+                           int64_t stride_key_head, int64_t stride_value_token,
+                           int64_t stride_value_head, int64_t stride_kc_block,
+                           int64_t stride_kc_slot, int64_t stride_kc_head,
+                           int64_t stride_vc_block, int64_t stride_vc_slot,
+                           int64_t stride_vc_head, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

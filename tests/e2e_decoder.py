@@ -1,0 +1,159 @@
+"""A small random-init Llama-shaped decoder built only from torch.ops.fxpr.*
+(test harness): embedding -> [RMSNorm -> q/k/v GEMMs -> RoPE -> KV-cache
+write -> paged attention -> o GEMM -> residual RMSNorm -> gate/up GEMMs ->
+SiLU * up -> down GEMM] x L -> final RMSNorm -> lm_head GEMM ->
+log_softmax_fxp -> greedy argmax.
+
+Every reduction runs in a fixed-point kernel; the rest (embedding lookup,
+RoPE, SiLU, products) is elementwise, so a request's tokens must not depend on
+which other requests share its batch or whether they are prefilling or
+decoding. The continuous-batching scheduler here runs any mix of prefills and
+decodes in one flat token batch, like vLLM's.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+
+@dataclass
+class Config:
+    vocab: int = 1024
+    hidden: int = 256
+    layers: int = 2
+    heads: int = 4
+    kv_heads: int = 2
+    head_dim: int = 64
+    ffn: int = 512
+    page: int = 16
+    pages: int = 512
+    eps: float = 1e-6
+    int_bits: int = 32
+    frac_bits: int = 16
+    dtype: torch.dtype = torch.bfloat16
+
+
+def _rand(g, *shape, std):
+    return (torch.randn(*shape, generator=g) * std)
+
+
+class TinyDecoder:
+    def __init__(self, cfg: Config, seed: int = 0, device: str = "cuda"):
+        self.cfg, self.dev = cfg, device
+        g = torch.Generator("cpu").manual_seed(seed)
+        d, c = cfg.dtype, cfg
+        w = lambda *s, std=0.02: _rand(g, *s, std=std).to(d).to(device)  # noqa: E731
+        self.embed = w(c.vocab, c.hidden, std=1.0)
+        self.layers = []
+        for _ in range(c.layers):
+            self.layers.append({
+                "ln1": (1 + _rand(g, c.hidden, std=0.1)).to(d).to(device),
+                "wq": w(c.heads * c.head_dim, c.hidden), "wk": w(c.kv_heads * c.head_dim, c.hidden),
+                "wv": w(c.kv_heads * c.head_dim, c.hidden), "wo": w(c.hidden, c.heads * c.head_dim),
+                "ln2": (1 + _rand(g, c.hidden, std=0.1)).to(d).to(device),
+                "wg": w(c.ffn, c.hidden), "wu": w(c.ffn, c.hidden), "wd": w(c.hidden, c.ffn),
+            })
+        self.ln_f = (1 + _rand(g, c.hidden, std=0.1)).to(d).to(device)
+        self.lm_head = w(c.vocab, c.hidden)
+        # one KV cache per layer; pages handed out per request
+        self.kv = [torch.zeros(c.pages, 2, c.page, c.kv_heads, c.head_dim, dtype=d, device=device)
+                   for _ in range(c.layers)]
+        inv = 1.0 / (10000.0 ** (torch.arange(0, c.head_dim, 2, dtype=torch.float32) / c.head_dim))
+        self.inv_freq = inv.to(device)
+
+    def _gemm(self, x, w):  # x [T, K], w [N, K] (vLLM layout) -> [T, N]
+        c = self.cfg
+        return torch.ops.fxpr.gemm_fxp(x, w.t(), None, c.int_bits, c.frac_bits)
+
+    def _rope(self, x, pos):  # x [T, H, D], rotate-half, fp32 math per element
+        ang = pos.to(torch.float32)[:, None] * self.inv_freq[None, :]
+        cos, sin = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+        xf = x.float()
+        x1, x2 = xf[..., : x.shape[-1] // 2], xf[..., x.shape[-1] // 2:]
+        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
+
+    def step(self, tokens, positions, qsl, seq_lens, block_table, slots, max_q):
+        """One forward over a flat batch; returns fixed-point log-probs [T, vocab]."""
+        c = self.cfg
+        T = tokens.shape[0]
+        h = self.embed[tokens]
+        residual = None
+        for li, L in enumerate(self.layers):
+            if residual is None:
+                residual = h.clone()
+                x = torch.ops.fxpr.rms_norm_fxp(h, L["ln1"], c.eps)
+            else:
+                x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, L["ln1"], c.eps)
+            q = self._rope(self._gemm(x, L["wq"]).view(T, c.heads, c.head_dim), positions)
+            k = self._rope(self._gemm(x, L["wk"]).view(T, c.kv_heads, c.head_dim), positions)
+            v = self._gemm(x, L["wv"]).view(T, c.kv_heads, c.head_dim)
+            torch.ops.fxpr.reshape_and_cache(k, v, self.kv[li], slots)
+            o = torch.empty_like(q)
+            torch.ops.fxpr.unified_attention_fxp(q, self.kv[li], o, qsl, seq_lens, block_table, max_q, None,
+                                                 True, c.head_dim ** -0.5, c.int_bits, c.frac_bits, 0.0, 0, 0)
+            h = self._gemm(o.view(T, -1), L["wo"])
+            x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, L["ln2"], c.eps)
+            gate, up = self._gemm(x, L["wg"]), self._gemm(x, L["wu"])
+            h = self._gemm((torch.nn.functional.silu(gate.float()) * up.float()).to(c.dtype), L["wd"])
+        x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, self.ln_f, c.eps)
+        logits = self._gemm(x, self.lm_head)
+        return torch.ops.fxpr.log_softmax_fxp(logits, c.int_bits, c.frac_bits, torch.float32)
+
+
+@dataclass
+class Request:
+    rid: int
+    prompt: list[int]
+    max_new: int
+    pages: list[int] = field(default_factory=list)
+    tokens: list[int] = field(default_factory=list)   # prompt + generated
+    cached: int = 0                                   # tokens already in the KV cache
+    logprobs: list[torch.Tensor] = field(default_factory=list)
+
+    @property
+    def done(self):
+        return len(self.tokens) - len(self.prompt) >= self.max_new
+
+
+def run(model: TinyDecoder, prompts: list[list[int]], max_new: int, schedule) -> dict[int, Request]:
+    """Greedy generation. ``schedule(step, active) -> list of requests`` picks
+    which unfinished requests run in each forward (a prefill runs the whole
+    uncached prompt, a decode one token)."""
+    c = model.cfg
+    reqs = {i: Request(i, p, max_new, tokens=list(p)) for i, p in enumerate(prompts)}
+    free = list(range(c.pages))
+    max_pages = -(-max(len(p) + max_new for p in prompts) // c.page)
+    step = 0
+    while any(not r.done for r in reqs.values()):
+        batch = schedule(step, [r for r in reqs.values() if not r.done])
+        step += 1
+        if not batch:
+            continue
+        toks, pos, slots, qsl, sls, bts = [], [], [], [0], [], []
+        for r in batch:
+            new = r.tokens[r.cached:]
+            need = -(-len(r.tokens) // c.page)
+            while len(r.pages) < need:
+                r.pages.append(free.pop(0))
+            for j, t in enumerate(new):
+                p = r.cached + j
+                toks.append(t)
+                pos.append(p)
+                slots.append(r.pages[p // c.page] * c.page + p % c.page)
+            qsl.append(qsl[-1] + len(new))
+            sls.append(len(r.tokens))
+            bts.append(r.pages + [0] * (max_pages - len(r.pages)))
+        dev = model.dev
+        lp = model.step(torch.tensor(toks, device=dev), torch.tensor(pos, device=dev),
+                        torch.tensor(qsl, dtype=torch.int32, device=dev),
+                        torch.tensor(sls, dtype=torch.int32, device=dev),
+                        torch.tensor(bts, dtype=torch.int32, device=dev),
+                        torch.tensor(slots, dtype=torch.int64, device=dev), max(qsl[i + 1] - qsl[i] for i in range(len(batch))))
+        for i, r in enumerate(batch):
+            last = lp[qsl[i + 1] - 1]
+            r.logprobs.append(last.cpu())
+            r.cached = len(r.tokens)
+            r.tokens.append(int(torch.argmax(last)))
+    return reqs

@@ -2,10 +2,11 @@
 
 The six reference schemas are kept verbatim (fxpr_vllm/_lib.py:13-33 of the
 reference) so callers and torch.compile graphs are a drop-in; PyTorch-ROCm
-dispatches HIP tensors through the CUDA key. Two schemas are new in this
+dispatches HIP tensors through the CUDA key. Three schemas are new in this
 build: fixed_row_sum (the integer sum the reference's tests do with torch,
-_tests/test_sum.py:12-16) and log_softmax_fxp (listed in the reference
-README.md:60 but not shipped). Validation and error classes follow the
+_tests/test_sum.py:12-16), log_softmax_fxp (listed in the reference
+README.md:60 but not shipped) and reshape_and_cache (the KV-cache write the
+reference backend takes from vLLM, attention_backend.py:253-277). Validation and error classes follow the
 reference impls (_lib.py:36-129).
 """
 
@@ -14,6 +15,7 @@ from __future__ import annotations
 import torch
 
 from ._kernels import attention as _attention
+from ._kernels import cache as _cache
 from ._kernels import casts as _casts
 from ._kernels import gemm as _gemm
 from ._kernels import rows as _rows
@@ -43,6 +45,10 @@ _lib.define("fixed_row_sum(Tensor q, int int_bits) -> Tensor")
 _lib.define(
     "log_softmax_fxp(Tensor x, int fxp_int_bits, int fxp_frac_bits, "
     "ScalarType? out_dtype=None) -> Tensor"
+)
+_lib.define(
+    "reshape_and_cache(Tensor key, Tensor value, Tensor(a!) kv_cache, "
+    "Tensor slot_mapping) -> ()"
 )
 
 
@@ -111,6 +117,11 @@ def _log_softmax_fxp_cuda(x: torch.Tensor, fxp_int_bits: int, fxp_frac_bits: int
     return _rows.log_softmax_fxp_run(x, int(fxp_int_bits), int(fxp_frac_bits), out_dtype)
 
 
+def _reshape_and_cache_cuda(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
+                            slot_mapping: torch.Tensor):
+    _cache.reshape_and_cache_run(key, value, kv_cache, slot_mapping)
+
+
 # Register after definition so the functions stay importable by name.
 _lib.impl("float_to_fixed", _float_to_fixed_cuda, "CUDA")
 _lib.impl("fixed_to_float", _fixed_to_float_cuda, "CUDA")
@@ -120,3 +131,4 @@ _lib.impl("gemm_fxp", _gemm_fxp_cuda, "CUDA")
 _lib.impl("unified_attention_fxp", _unified_attention_fxp_cuda, "CUDA")
 _lib.impl("fixed_row_sum", _fixed_row_sum_cuda, "CUDA")
 _lib.impl("log_softmax_fxp", _log_softmax_fxp_cuda, "CUDA")
+_lib.impl("reshape_and_cache", _reshape_and_cache_cuda, "CUDA")

@@ -75,6 +75,11 @@ def _log_softmax_fxp_fake(x, fxp_int_bits, fxp_frac_bits, out_dtype=None):
     return torch.empty_like(x, dtype=x.dtype if out_dtype is None else out_dtype)
 
 
+@torch.library.register_fake("fxpr::reshape_and_cache")
+def _reshape_and_cache_fake(key, value, kv_cache, slot_mapping):
+    return None
+
+
 gemm_fxp = torch.ops.fxpr.gemm_fxp
 rms_norm_fxp = torch.ops.fxpr.rms_norm_fxp
 rms_norm_fxp_residual = torch.ops.fxpr.rms_norm_fxp_residual
@@ -82,3 +87,5 @@ float_to_fixed = torch.ops.fxpr.float_to_fixed
 fixed_to_float = torch.ops.fxpr.fixed_to_float
 fixed_row_sum = torch.ops.fxpr.fixed_row_sum
 log_softmax_fxp = torch.ops.fxpr.log_softmax_fxp
+reshape_and_cache = torch.ops.fxpr.reshape_and_cache
+unified_attention_fxp = torch.ops.fxpr.unified_attention_fxp
