@@ -369,9 +369,12 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, 
 // increasing k, zero C at each 128-wide K-tile), so results are bitwise
 // identical to every other configuration; only the schedule differs.
 //
-// 8 waves (two per SIMD) over a 256 x 128 workgroup tile, 64 x 64 per wave.
+// Waves of 64 x 64 outputs, two per SIMD: one 8-wave workgroup per CU over a
+// 256 x 128 tile with three LDS stages, or two 4-wave workgroups per CU over
+// 128 x 128 tiles with two stages each (the two waves of a SIMD then belong
+// to different workgroups and never wait on the same barrier).
 // A and B stages (64 k) go straight from global memory into LDS with
-// global_load_lds_dwordx4 (no staging registers), three stages in flight.
+// global_load_lds_dwordx4 (no staging registers).
 // Rows are 128 B with the 16-byte chunk c of row r stored at slot
 // c ^ ((r >> 1) & 7): each DMA instruction fills 1 KB of LDS contiguously,
 // and the 16-row fragment reads hit 16 distinct 16-byte bank groups.
@@ -383,17 +386,22 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, 
 // first (integer sums do not depend on the order of tiles). The epilogue
 // stages each wave's C tile through LDS to write whole 16-byte row pieces.
 
-template <int BM_, int BN_, int WGM_, int WGN_> struct BigTile {
+template <int BM_, int BN_, int WGM_, int WGN_, int NS_, int WPE_ = 2> struct BigTile {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+  static constexpr int NS = NS_;    // LDS stages (DMAs run NS - 1 stages ahead)
+  static constexpr int WPE = WPE_;  // waves per SIMD the register budget is sized for
   static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
   static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int MB = WM / 16, NB = WN / 16;
 };
-using TB = BigTile<256, 128, 4, 2>;
-constexpr int kBigStages = 3;
+using TB = BigTile<256, 128, 4, 2, 3>;   // one 8-wave workgroup per CU
+using TB2 = BigTile<128, 128, 2, 2, 2>;  // two 4-wave workgroups per CU
+// int64 accumulators double the integer state (64 x 64 outputs need 128
+// registers of it): one wave per SIMD, one 4-wave workgroup per CU
+using TB64 = BigTile<128, 128, 2, 2, 3, 1>;
 
 template <class BT> constexpr size_t big_lds_bytes() {
-  constexpr size_t stages = size_t(kBigStages) * (BT::BM + BT::BN) * 128;
+  constexpr size_t stages = size_t(BT::NS) * (BT::BM + BT::BN) * 128;
   constexpr size_t epi = size_t(BT::WAVES) * BT::WM * (BT::WN + 8) * 2;
   return stages > epi ? stages : epi;
 }
@@ -401,7 +409,7 @@ template <class BT> constexpr size_t big_lds_bytes() {
 typedef __attribute__((address_space(3))) void* LdsPtr;
 
 template <int DT, int BITS, class BT, bool SPLIT>
-__global__ __launch_bounds__(BT::THREADS) void gemm_big_kernel(GemmArgs args) {
+__global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs args) {
   using M_ = Mma<DT>;
   using T = typename M_::T;
   using AccT = typename Acc<BITS>::T;
@@ -575,14 +583,15 @@ __global__ __launch_bounds__(BT::THREADS) void gemm_big_kernel(GemmArgs args) {
   const int nst = 2 * nfull;
   if (nst > 0) {
     u32x4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
-    dma(0, 0);
-    dma(min(1, nst - 1), 1);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
+    constexpr int NS = BT::NS;
+#pragma unroll
+    for (int i = 0; i + 1 < NS; ++i) dma(min(i, nst - 1), i);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA * (NS - 2)) : "memory");
     __builtin_amdgcn_s_barrier();
     read_frags(0, 0, fa0, fb0);
     auto stage = [&](int s, bool tile_start) {
-      const int buf = s % kBigStages;
-      dma(min(s + 2, nst - 1), (s + 2) % kBigStages);
+      const int buf = s % NS;
+      dma(min(s + NS - 1, nst - 1), (s + NS - 1) % NS);
       lds_wait(fa0, fb0);
       const unsigned aa1 = frag_addr(buf, 1, false), bb1 = frag_addr(buf, 1, true);
       __builtin_amdgcn_sched_barrier(0);
@@ -610,13 +619,13 @@ __global__ __launch_bounds__(BT::THREADS) void gemm_big_kernel(GemmArgs args) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) mma(i, j, fa1[i], fb1[j], false);
       __builtin_amdgcn_sched_barrier(0);
-      // Own DMAs of stage s + 1 landed; the barrier covers everyone's, and
-      // everyone's reads of stage s are done (buffer s % 3 is refilled two
-      // stages later). A plain s_barrier: __syncthreads() would also fence,
-      // i.e. wait for the DMAs of stage s + 2 as well.
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
+      // Own DMAs of stage s + 1 landed (only later stages' may be in
+      // flight); the barrier covers everyone's, and everyone's reads of stage
+      // s are done (its buffer is refilled NS - 1 stages later). A plain
+      // s_barrier: __syncthreads() would also fence, i.e. wait for every DMA.
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA * (NS - 2)) : "memory");
       __builtin_amdgcn_s_barrier();
-      read_frags((s + 1) % kBigStages, 0, fa0, fb0);
+      read_frags((s + 1) % NS, 0, fa0, fb0);
     };
     for (int s = 0; s < nst; s += 2) {
       stage(s, true);
@@ -785,8 +794,16 @@ inline void tile_dims(TileId t, int& bm, int& bn) {
 template <int DT, int BITS>
 int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
   const TileId t = pick_tile(a.M);
+  if constexpr (DT != FXPR_DTYPE_F32 && BITS == 64) {
+    if (vec && !b_ncontig && t == TileId::Big) return launch_big<DT, BITS, TB64>(a, splits, st);
+  }
   if constexpr (DT != FXPR_DTYPE_F32 && BITS != 64) {
-    if (vec && !b_ncontig && t == TileId::Big) return launch_big<DT, BITS, TB>(a, splits, st);
+    if (vec && !b_ncontig && t == TileId::Big) {
+      // two 4-wave workgroups per CU from M = 1024 (6 % faster at M = 8192),
+      // one 8-wave workgroup below (fewer, larger tiles while HBM-bound)
+      if (a.M >= 1024) return launch_big<DT, BITS, TB2>(a, splits, st);
+      return launch_big<DT, BITS, TB>(a, splits, st);
+    }
   }
   if (vec && !b_ncontig) {
     switch (t) {
@@ -827,8 +844,8 @@ inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int req
     int bm, bn;
     tile_dims(pick_tile(M), bm, bn);
     if (pick_tile(M) == TileId::Big && io_dtype != FXPR_DTYPE_F32) {
-      bm = TB::BM;
-      bn = TB::BN;
+      bm = M >= 1024 ? TB2::BM : TB::BM;
+      bn = M >= 1024 ? TB2::BN : TB::BN;
     }
     const int64_t tiles = cdiv(M, bm) * cdiv(N, bn);
     if (tiles >= 256) return 1;
