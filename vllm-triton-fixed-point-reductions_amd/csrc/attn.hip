@@ -21,14 +21,28 @@ struct WsLayout {
   int64_t pmax = -1, den = -1, wv = -1, scores = -1, total = 0;
 };
 
-WsLayout ws_layout(int64_t num_tokens, int num_heads, int num_kv_heads, int head_dim, int int_bits,
-                   int splits, int max_query_len, int max_blocks, int page_size) {
+// Score cache geometry: per (request, kv head) cdiv(lmax, TILE) key tiles,
+// each 4 waves x score_kg lane groups x 256 bytes.
+struct ScoreGeom {
+  int64_t tiles, kg, bytes;
+};
+
+ScoreGeom score_geom(int num_requests, int num_kv_heads, int group, int max_query_len, int64_t lmax) {
+  const int64_t rows = int64_t(max_query_len > 1 ? max_query_len : 1) * group;
+  ScoreGeom sg;
+  sg.tiles = cdiv(lmax, TILE);
+  sg.kg = cdiv(rows < QROWS ? rows : QROWS, 4);
+  sg.bytes = rows <= QROWS ? int64_t(num_requests) * num_kv_heads * sg.tiles * 4 * sg.kg * 256 : -1;
+  return sg;
+}
+
+WsLayout ws_layout(int num_requests, int64_t num_tokens, int num_heads, int num_kv_heads, int head_dim,
+                   int int_bits, int splits, int max_query_len, int max_blocks, int page_size) {
   WsLayout w;
   const int group = num_heads / num_kv_heads;
   const int64_t lmax = int64_t(max_blocks) * page_size;
-  const int64_t score_bytes = num_tokens * num_heads * lmax * 4;
-  const bool cache = int64_t(max_query_len > 1 ? max_query_len : 1) * group <= QROWS &&
-                     score_bytes <= kScoreCacheMax;
+  const int64_t score_bytes = score_geom(num_requests, num_kv_heads, group, max_query_len, lmax).bytes;
+  const bool cache = score_bytes >= 0 && score_bytes <= kScoreCacheMax;
   if (splits <= 1 && !cache) return w;
   const int64_t rows = num_tokens * num_heads * splits;
   w.pmax = 0;
@@ -94,8 +108,8 @@ extern "C" int64_t fxpr_attention_workspace_bytes(int num_requests, int64_t num_
     return 0;
   const SplitPlan sp = plan_splits(num_requests, num_kv_heads, num_heads / num_kv_heads, max_query_len,
                                    max_blocks_per_seq, page_size, num_kv_splits);
-  return ws_layout(num_tokens, num_heads, num_kv_heads, head_dim, int_bits, sp.splits, max_query_len,
-                   max_blocks_per_seq, page_size).total;
+  return ws_layout(num_requests, num_tokens, num_heads, num_kv_heads, head_dim, int_bits, sp.splits,
+                   max_query_len, max_blocks_per_seq, page_size).total;
 }
 
 extern "C" int fxpr_unified_attention(
@@ -131,7 +145,7 @@ extern "C" int fxpr_unified_attention(
   // the kernels form cache offsets as 32 x 32 -> 64-bit products
   for (int64_t sv : {stride_k_block, stride_k_slot, stride_k_head, stride_v_block, stride_v_slot, stride_v_head})
     if (sv < 0 || sv > int64_t(0xffffffff)) return FXPR_E_ARG;
-  const WsLayout wl = ws_layout(num_tokens, num_heads, num_kv_heads, head_dim, int_bits, num_splits,
+  const WsLayout wl = ws_layout(num_requests, num_tokens, num_heads, num_kv_heads, head_dim, int_bits, num_splits,
                                 max_query_len, max_blocks_per_seq, page_size);
   if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return FXPR_E_WORKSPACE;
 
@@ -149,8 +163,12 @@ extern "C" int fxpr_unified_attention(
   if (wl.den >= 0) a.den_ws = base + wl.den;
   if (wl.wv >= 0) a.wv_ws = base + wl.wv;
   if (wl.scores >= 0) {
+    const ScoreGeom sg = score_geom(num_requests, num_kv_heads, num_heads / num_kv_heads, max_query_len,
+                                    int64_t(max_blocks_per_seq) * page_size);
     a.scores = reinterpret_cast<float*>(base + wl.scores);
-    a.score_bytes = int(num_tokens * num_heads * int64_t(max_blocks_per_seq) * page_size * 4);
+    a.score_bytes = int(sg.bytes);
+    a.score_tiles = int(sg.tiles);
+    a.score_kg = int(sg.kg);
   }
   a.sq_t = stride_q_token;
   a.sq_h = stride_q_head;

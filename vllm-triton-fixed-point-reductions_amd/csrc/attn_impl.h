@@ -52,7 +52,7 @@ struct AttnArgs {
   const int32_t* bt;
   const float* alibi;  // per q head, already multiplied by log2(e); or null
   float* pmax;         // [T, Hq, S]
-  float* scores;       // [T, Hq, lmax] cached pass-1 scores, or null
+  float* scores;       // cached pass-1 scores (layout: see the kernel), or null
   void* den_ws;        // [T, Hq, S]     (int32 or int64)
   void* wv_ws;         // [T, Hq, S, D]  (int32 or int64)
   int64_t sq_t, sq_h, sk_b, sk_s, sk_h, sv_b, sv_s, sv_h, so_t, so_h, sbt;
@@ -65,6 +65,8 @@ struct AttnArgs {
   int64_t lmax;         // key capacity of a block-table row (max_blocks * page_size)
   int ps_shift;         // log2(page_size) if a power of two, else -1
   int score_bytes;      // size of the score cache (< 2^31), or 0
+  int score_tiles;      // key tiles per (request, kv head) in the score cache
+  int score_kg;         // 4-row lane groups per (request, kv head) in the score cache
   float scale_log2, softcap_log2, fxp_scale, fxp_inv;
 };
 
@@ -292,22 +294,19 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     }
   };
 
-  // Cached scores: [T, Hq, lmax] fp32, written by pass 1, read by pass 2.
-  // Row bases of the lane's four rows; rows outside the request point at a
-  // real row of the workgroup (pass 2 reads the same cache lines as that
-  // row and discards the values; pass 1 never stores them).
-  float* sbase[4] = {nullptr, nullptr, nullptr, nullptr};
-  uint32_t soff[4] = {0u, 0u, 0u, 0u};  // byte offsets of the rows
-  if (cached && (MODE == MAXPASS || MODE == ACCCACHED)) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      RowInfo rr = srow[e];
-      if (!rr.valid) rr = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + min(e, rows_total - row0 - 1));
-      const int64_t idx = (rr.token * a.num_heads + rr.head) * a.lmax;
-      sbase[e] = a.scores + idx;
-      soff[e] = uint32_t(idx * 4);
-    }
-  }
+  // Cached scores (decode-shaped launches: one 16-row q-tile per (request,
+  // kv head)), written by pass 1 and read back by pass 2 in the MFMA score
+  // layout itself: per (request, kv head, key tile, wave, lane group kg) a
+  // 256-byte block in which lane key k holds its four rows' scores as one
+  // 16-byte vector. Stores and loads are then whole lines; lane groups whose
+  // rows are all outside the q-tile (kg >= score_kg) have no block.
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(a.scores, 0, a.score_bytes, kBufferWord3);
+  const uint32_t sc_rg = uint32_t(r * a.num_kv_heads + g) * uint32_t(a.score_tiles);
+  auto sc_off = [&](int t) -> int {  // byte offset of the lane's vector for tile t, or out of range
+    const bool ok = kg < a.score_kg && t < a.score_tiles;
+    const uint32_t blk = ((sc_rg + uint32_t(t)) * 4u + uint32_t(wave)) * uint32_t(a.score_kg) + uint32_t(kg);
+    return ok ? int(blk * 256u + uint32_t(lane & 15) * 16u) : int(0x80000000u);
+  };
 
   // ---------------- pass 1: row maxima (and cached scores) ----------------
   float m[4];
@@ -329,8 +328,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
       KFrag kb[R1][QSTEPS];
       int eb[R1];
       auto tl = [&](int x) { return min(x, my_hi - 1); };
-      const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(a.scores, 0, a.score_bytes, kBufferWord3);
-      const int kmax = min(seq_len, int(a.lmax < 0x7fffffff ? a.lmax : 0x7fffffff));
 #pragma unroll
       for (int i = 0; i < R1; ++i) eb[i] = k_entry(tl(my_lo + i));
 #pragma unroll
@@ -347,16 +344,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
           const bool live = t + u < my_hi;
           float s[4];
           k_scores(t + u, kb[u], s);
-          const int key = (t + u) * TILE + wave * 16 + (lane & 15);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             s[e] = live ? s[e] : -__builtin_inff();
-            if (MODE == MAXPASS && cached) {
-              const bool st = live && srow[e].valid && key < kmax;
-              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s[e]), srsrc,
-                                                    st ? int(soff[e] + uint32_t(key) * 4u) : int(0x80000000u), 0, 0);
-            }
             mx[e] = fmaxf(mx[e], s[e]);
+          }
+          if (MODE == MAXPASS && cached) {
+            const u32x4 v = {__builtin_bit_cast(uint32_t, s[0]), __builtin_bit_cast(uint32_t, s[1]),
+                             __builtin_bit_cast(uint32_t, s[2]), __builtin_bit_cast(uint32_t, s[3])};
+            __builtin_amdgcn_raw_buffer_store_b128(v, srsrc, live ? sc_off(t + u) : int(0x80000000u), 0, 0);
           }
         }
       }
@@ -427,12 +423,14 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   };
   auto s_load = [&](int t, float (&s)[4]) {
     const int key = t * TILE + wave * 16 + (lane & 15);
-    const int64_t kc = key < a.lmax ? key : a.lmax - 1;
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(srsrc, sc_off(t), 0, 0);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float x = sbase[e][kc];
-      s[e] = (srow[e].valid && key >= srow[e].kstart && key < srow[e].kend && key < a.lmax) ? x
-                                                                                           : -__builtin_inff();
+      // element copied out first: __builtin_bit_cast of a vector element
+      // lvalue reads the vector's first element whatever the index
+      const uint32_t x = v[e];
+      s[e] = (srow[e].valid && key >= srow[e].kstart && key < srow[e].kend) ? __builtin_bit_cast(float, x)
+                                                                             : -__builtin_inff();
     }
   };
 
