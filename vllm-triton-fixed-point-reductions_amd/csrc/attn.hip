@@ -8,73 +8,57 @@ using namespace fxpr::attn;
 namespace {
 
 constexpr int kMaxSplits = 64;
-constexpr int64_t kScoreCacheMax = int64_t(512) << 20;  // bytes
+// Split launches keep per-chunk partials; above this many bytes of them a
+// launch runs unsplit instead (split counts never change the bits).
+constexpr int64_t kSplitWsMax = int64_t(1) << 30;
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 inline int acc_bytes(int int_bits) { return int_bits == 64 ? 8 : 4; }
 
-// Workspace layout: per-split maxima, per-split integer partials (only with
-// more than one split) and the cached pass-1 scores (decode-shaped launches:
-// one 16-row q-tile per (request, kv head), when they fit kScoreCacheMax).
-struct WsLayout {
-  int64_t pmax = -1, den = -1, wv = -1, scores = -1, total = 0;
-};
-
-// Score cache geometry: per (request, kv head) cdiv(lmax, TILE) key tiles,
-// each 4 waves x score_kg lane groups x 256 bytes.
-struct ScoreGeom {
-  int64_t tiles, kg, bytes;
-};
-
-ScoreGeom score_geom(int num_requests, int num_kv_heads, int group, int max_query_len, int64_t lmax) {
-  const int64_t rows = int64_t(max_query_len > 1 ? max_query_len : 1) * group;
-  ScoreGeom sg;
-  sg.tiles = cdiv(lmax, TILE);
-  sg.kg = cdiv(rows < QROWS ? rows : QROWS, 4);
-  sg.bytes = rows <= QROWS ? int64_t(num_requests) * num_kv_heads * sg.tiles * 4 * sg.kg * 256 : -1;
-  return sg;
+// Chunks per row that a block-table row of max_blocks pages can hold.
+inline int64_t chunk_slots(int max_blocks, int page_size) {
+  return cdiv(cdiv(int64_t(max_blocks) * page_size, TILE), CT);
 }
 
-WsLayout ws_layout(int num_requests, int64_t num_tokens, int num_heads, int num_kv_heads, int head_dim,
-                   int int_bits, int splits, int max_query_len, int max_blocks, int page_size) {
+// Split-launch workspace: per (token, head) the chunk range, and per
+// (token, head, chunk) the row maximum, the integer denominator and the
+// integer weighted V row. Unsplit launches need none.
+struct WsLayout {
+  int64_t crange = -1, pmax = -1, den = -1, wv = -1, total = 0;
+};
+
+WsLayout ws_layout(int64_t num_tokens, int num_heads, int head_dim, int int_bits, int splits, int64_t slots) {
   WsLayout w;
-  const int group = num_heads / num_kv_heads;
-  const int64_t lmax = int64_t(max_blocks) * page_size;
-  const int64_t score_bytes = score_geom(num_requests, num_kv_heads, group, max_query_len, lmax).bytes;
-  const bool cache = score_bytes >= 0 && score_bytes <= kScoreCacheMax;
-  if (splits <= 1 && !cache) return w;
-  const int64_t rows = num_tokens * num_heads * splits;
-  w.pmax = 0;
-  w.total = align256(rows * 4);
-  if (splits > 1) {
-    w.den = w.total;
-    w.total += align256(rows * acc_bytes(int_bits));
-    w.wv = w.total;
-    w.total += align256(rows * head_dim * acc_bytes(int_bits));
-  }
-  if (cache) {
-    w.scores = w.total;
-    w.total += align256(score_bytes);
-  }
+  if (splits <= 1) return w;
+  const int64_t rows = num_tokens * num_heads;
+  w.crange = 0;
+  w.total = align256(rows * 8);
+  w.pmax = w.total;
+  w.total += align256(rows * slots * 4);
+  w.den = w.total;
+  w.total += align256(rows * slots * acc_bytes(int_bits));
+  w.wv = w.total;
+  w.total += align256(rows * slots * head_dim * acc_bytes(int_bits));
   return w;
 }
 
 }  // namespace
 
-// Split policy. An explicit request wins (key tiles dealt evenly over the
-// splits, as the reference's _split_tile_range does). Automatic (0), after
-// the reference's _pick_num_splits (attention.py:664-689): no split for short
-// contexts (<= 32 key tiles) or when the (request, kv-head, q-tile)
-// workgroups already oversubscribe the 256 CUs; otherwise splits of a fixed
-// kSplitTiles key tiles each, so every workgroup carries about the same work
-// whatever its request's length (requests shorter than the longest get empty
-// splits, which only write neutral partials). Split counts never change bits.
+// Split policy. An explicit request wins (each workgroup's key chunks dealt
+// evenly over the splits, as the reference's _split_tile_range deals tiles).
+// Automatic (0), after the reference's _pick_num_splits
+// (attention.py:664-689): no split for short contexts (<= 32 key tiles) or
+// when the (request, kv-head, q-tile) workgroups already oversubscribe the
+// 256 CUs; otherwise splits of a fixed kSplitChunks chunks each, so every
+// workgroup carries about the same work whatever its request's length
+// (requests shorter than the longest get empty splits). Split counts never
+// change bits.
 namespace {
-constexpr int kSplitTiles = 16;
+constexpr int kSplitChunks = 2;
 
 struct SplitPlan {
-  int splits, tiles_per_split;
+  int splits, chunks_per_split;
 };
 
 SplitPlan plan_splits(int num_requests, int num_kv_heads, int group, int max_query_len, int max_blocks,
@@ -85,10 +69,24 @@ SplitPlan plan_splits(int num_requests, int num_kv_heads, int group, int max_que
   const int64_t qtiles = cdiv(int64_t(max_query_len > 1 ? max_query_len : 1) * group, QROWS);
   const int64_t base = int64_t(num_requests > 1 ? num_requests : 1) * num_kv_heads * qtiles;
   if (base > 8 * 256) return {1, 0};
-  int64_t s = cdiv(tiles, kSplitTiles);
+  const int64_t chunks = cdiv(tiles, CT);
+  int64_t s = cdiv(chunks, kSplitChunks);
   if (s > kMaxSplits) s = kMaxSplits;
-  const int per = int(cdiv(tiles, s));
-  return {int(s), per};
+  if (s <= 1) return {1, 0};
+  return {int(s), int(cdiv(chunks, s))};
+}
+
+// The plan a launch runs: plan_splits, unsplit when the partials would exceed
+// kSplitWsMax.
+SplitPlan launch_plan(int num_requests, int64_t num_tokens, int num_heads, int num_kv_heads, int head_dim,
+                      int int_bits, int max_query_len, int max_blocks, int page_size, int requested) {
+  SplitPlan sp = plan_splits(num_requests, num_kv_heads, num_heads / num_kv_heads, max_query_len, max_blocks,
+                             page_size, requested);
+  if (sp.splits > 1 &&
+      ws_layout(num_tokens, num_heads, head_dim, int_bits, sp.splits, chunk_slots(max_blocks, page_size)).total >
+          kSplitWsMax)
+    sp = {1, 0};
+  return sp;
 }
 }  // namespace
 
@@ -106,10 +104,11 @@ extern "C" int64_t fxpr_attention_workspace_bytes(int num_requests, int64_t num_
   if (num_requests <= 0 || num_tokens <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
       max_blocks_per_seq <= 0 || page_size <= 0 || num_heads % num_kv_heads != 0 || num_kv_splits < 0)
     return 0;
-  const SplitPlan sp = plan_splits(num_requests, num_kv_heads, num_heads / num_kv_heads, max_query_len,
-                                   max_blocks_per_seq, page_size, num_kv_splits);
-  return ws_layout(num_requests, num_tokens, num_heads, num_kv_heads, head_dim, int_bits, sp.splits,
-                   max_query_len, max_blocks_per_seq, page_size).total;
+  const SplitPlan sp = launch_plan(num_requests, num_tokens, num_heads, num_kv_heads, head_dim, int_bits,
+                                   max_query_len, max_blocks_per_seq, page_size, num_kv_splits);
+  return ws_layout(num_tokens, num_heads, head_dim, int_bits, sp.splits,
+                   chunk_slots(max_blocks_per_seq, page_size))
+      .total;
 }
 
 extern "C" int fxpr_unified_attention(
@@ -128,8 +127,8 @@ extern "C" int fxpr_unified_attention(
     return FXPR_E_SHAPE;
   if (num_requests == 0 || num_tokens == 0) return FXPR_OK;
   if (max_blocks_per_seq <= 0 || num_blocks <= 0) return FXPR_E_SHAPE;
-  const SplitPlan sp = plan_splits(num_requests, num_kv_heads, num_heads / num_kv_heads, max_query_len,
-                                   max_blocks_per_seq, page_size, num_kv_splits);
+  const SplitPlan sp = launch_plan(num_requests, num_tokens, num_heads, num_kv_heads, head_dim, int_bits,
+                                   max_query_len, max_blocks_per_seq, page_size, num_kv_splits);
   const int num_splits = sp.splits;
   if (!q || !k_cache || !v_cache || !o || !query_start_loc || !seq_lens || !block_table) return FXPR_E_ARG;
   if (io_dtype != FXPR_DTYPE_BF16 && io_dtype != FXPR_DTYPE_F16 && io_dtype != FXPR_DTYPE_F32)
@@ -145,8 +144,9 @@ extern "C" int fxpr_unified_attention(
   // the kernels form cache offsets as 32 x 32 -> 64-bit products
   for (int64_t sv : {stride_k_block, stride_k_slot, stride_k_head, stride_v_block, stride_v_slot, stride_v_head})
     if (sv < 0 || sv > int64_t(0xffffffff)) return FXPR_E_ARG;
-  const WsLayout wl = ws_layout(num_requests, num_tokens, num_heads, num_kv_heads, head_dim, int_bits, num_splits,
-                                max_query_len, max_blocks_per_seq, page_size);
+  const int64_t slots = chunk_slots(max_blocks_per_seq, page_size);
+  if (slots > 0x7fffffff) return FXPR_E_SHAPE;
+  const WsLayout wl = ws_layout(num_tokens, num_heads, head_dim, int_bits, num_splits, slots);
   if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return FXPR_E_WORKSPACE;
 
   AttnArgs a{};
@@ -159,17 +159,11 @@ extern "C" int fxpr_unified_attention(
   a.bt = block_table;
   a.alibi = alibi_slopes;
   char* base = static_cast<char*>(workspace);
+  if (wl.crange >= 0) a.crange = reinterpret_cast<int*>(base + wl.crange);
   if (wl.pmax >= 0) a.pmax = reinterpret_cast<float*>(base + wl.pmax);
   if (wl.den >= 0) a.den_ws = base + wl.den;
   if (wl.wv >= 0) a.wv_ws = base + wl.wv;
-  if (wl.scores >= 0) {
-    const ScoreGeom sg = score_geom(num_requests, num_kv_heads, num_heads / num_kv_heads, max_query_len,
-                                    int64_t(max_blocks_per_seq) * page_size);
-    a.scores = reinterpret_cast<float*>(base + wl.scores);
-    a.score_bytes = int(sg.bytes);
-    a.score_tiles = int(sg.tiles);
-    a.score_kg = int(sg.kg);
-  }
+  a.chunk_slots = int(slots);
   a.sq_t = stride_q_token;
   a.sq_h = stride_q_head;
   a.sk_b = stride_k_block;
@@ -187,7 +181,7 @@ extern "C" int fxpr_unified_attention(
   a.head_dim = head_dim;
   a.page_size = page_size;
   a.num_splits = num_splits;
-  a.tiles_per_split = sp.tiles_per_split;
+  a.chunks_per_split = sp.chunks_per_split;
   a.window = window_size > 0 ? window_size : 0;
   a.causal = is_causal ? 1 : 0;
   a.max_blocks = max_blocks_per_seq;

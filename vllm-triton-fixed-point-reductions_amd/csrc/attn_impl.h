@@ -1,25 +1,35 @@
 // Paged prefill + decode attention with fixed-point cross-tile reductions
 // (gfx950 MFMA). Kernels are instantiated per input type in attn_*.hip.
 //
-// Per (request r, query row i, head h), keys n of the request's paged KV:
-//   s_n  = fl32(q . k_n) * scale*log2e  [softcap] [+ alibi*(n - qpos)],
-//          -inf where masked (causal n > qpos, window, n >= seq_len)
-//   m    = max_n s_n over every key of the row (all splits)
-//   w_n  = exp2(s_n - m)
-//   den  = sum_n RNE_sat(w_n * 2^f)                        (integer)
-//   wv_d = sum_tiles RNE_sat(fl32(sum_{n in tile} IO(w_n) v_n[d]) * 2^f)
-//   o_d  = IO(fl32(wv_d) 2^-f / max(fl32(den) 2^-f, 1e-6))
+// Per (request r, query row i, head h), keys n of the request's paged KV,
+// in absolute chunks C of CT*64 = 512 keys:
+//   s_n   = fl32(q . k_n) * scale*log2e  [softcap] [+ alibi*(n - qpos)],
+//           -inf where masked (causal n > qpos, window, n >= seq_len)
+//   m_C   = max_{n in C} s_n                 (the chunk's own row maximum)
+//   w_n   = exp2(s_n - m_C)
+//   den_C = sum_{n in C} RNE_sat(w_n * 2^f)                       (integer)
+//   wv_C  = sum_{tiles of C} RNE_sat(fl32(sum_{n in tile} IO(w_n) v_n[d]) * 2^f)
+//   fold the chunks in ascending order into (M, den, wv):
+//     M' = max(M, m_C), den' = rescale(den, 2^(M - M')) + rescale(den_C, 2^(m_C - M')),
+//     wv' likewise, rescale(x, f) = RNE_sat(fl64(x) * f)
+//   o_d   = IO(fl32(wv_d) 2^-f / max(fl32(den) 2^-f, 1e-6))
 // Replaces _attn_fused_kernel / _attn_split_max_kernel / _attn_split_dv_kernel
-// (fxpr_vllm/_triton/attention.py:127-301, 306-436, 440-652). Key tiles are
-// aligned to absolute key positions (64 keys for bf16/f16, 32 for f32, the
-// reference's BLOCK_N), and every score and tile partial comes from the same
-// MFMA chain for a given row whatever the workgroup's other rows, the split
-// count or the decode / prefill path, so outputs are bitwise invariant to all
-// of them. Splits exchange only the row maxima (pass 1) and integer partials
-// (pass 2, summed by a combine kernel): no atomics, nothing to pre-zero.
+// (fxpr_vllm/_triton/attention.py:127-301, 306-436, 440-652), which take every
+// weight against the row's global maximum and so read K twice (or exchange
+// maxima between splits first). Here each key is read once: a chunk's scores
+// stay in registers between its K and V halves. A row whose keys fit in one
+// chunk gets the reference's formula exactly. Key tiles (64 keys, the
+// quantised chains 64 keys for bf16/f16 and 32 for f32, the reference's
+// BLOCK_N) and chunks are aligned to absolute key positions, and every score,
+// tile partial and fold step comes from the same instruction sequence for a
+// given row whatever the workgroup's other rows, the split count or the
+// decode / prefill shape, so outputs are bitwise invariant to all of them.
+// Splits write per-chunk partials, folded by a combine kernel in the same
+// order: no atomics, nothing to pre-zero.
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "fxp_device.h"
 #include "fxpr_internal.h"
@@ -37,10 +47,8 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;  // 4 waves
 constexpr int TILE = 64;       // keys per iteration (and per split unit)
 constexpr int QROWS = 16;      // query rows (query x GQA head) per workgroup
-// Word 3 of a raw (untyped, unswizzled) buffer resource on gfx9-family GPUs.
-constexpr int kBufferWord3 = 0x00020000;
 
-enum Mode { FUSED = 0, MAXPASS = 1, ACCPASS = 2, ACCCACHED = 3 };
+constexpr int CT = 8;          // key tiles per chunk (the unit of the softmax statistics)
 
 struct AttnArgs {
   const void* q;
@@ -51,22 +59,20 @@ struct AttnArgs {
   const int32_t* seq_lens;
   const int32_t* bt;
   const float* alibi;  // per q head, already multiplied by log2(e); or null
-  float* pmax;         // [T, Hq, S]
-  float* scores;       // cached pass-1 scores (layout: see the kernel), or null
-  void* den_ws;        // [T, Hq, S]     (int32 or int64)
-  void* wv_ws;         // [T, Hq, S, D]  (int32 or int64)
+  float* pmax;         // [T, Hq, chunk_slots] per-chunk row maxima         (split launches)
+  void* den_ws;        // [T, Hq, chunk_slots] denominators, int32 / int64  (split launches)
+  void* wv_ws;         // [T, Hq, chunk_slots, D] weighted V, int32 / int64 (split launches)
+  int* crange;         // [T, Hq, 2] chunk range [first, end) of the row    (split launches)
   int64_t sq_t, sq_h, sk_b, sk_s, sk_h, sv_b, sv_s, sv_h, so_t, so_h, sbt;
   int num_heads, num_kv_heads, group, head_dim, page_size, num_splits, window, causal;
   int max_blocks;       // block-table row length
-  int tiles_per_split;  // > 0: fixed key tiles per split (work-balanced); 0: even division
+  int chunks_per_split;  // > 0: fixed chunks per split (work-balanced); 0: even division
+  int chunk_slots;       // chunks per row in the split workspace
   int num_requests;
   int64_t num_blocks;   // physical blocks in the cache
   int64_t num_tokens;   // rows of q / o
   int64_t lmax;         // key capacity of a block-table row (max_blocks * page_size)
   int ps_shift;         // log2(page_size) if a power of two, else -1
-  int score_bytes;      // size of the score cache (< 2^31), or 0
-  int score_tiles;      // key tiles per (request, kv head) in the score cache
-  int score_kg;         // 4-row lane groups per (request, kv head) in the score cache
   float scale_log2, softcap_log2, fxp_scale, fxp_inv;
 };
 
@@ -141,7 +147,42 @@ __device__ __forceinline__ RowInfo row_info(const AttnArgs& a, int g, int q_star
   return ri;
 }
 
-template <int DT, int BITS, int DMAX, int MODE>
+// Per-row statistics of key chunks are folded in fixed point: an accumulator
+// (wrapped to BITS) times f <= 1, rounded half-to-even in fp64 and saturated.
+// Shared by the kernel's in-register merge and the combine kernel, so both
+// produce the same bits.
+template <int BITS> __device__ __forceinline__ typename AccOf<BITS>::T rescale(typename AccOf<BITS>::T x, float f) {
+  double xv;
+  if constexpr (BITS == 16) xv = static_cast<double>(static_cast<int16_t>(x));
+  else xv = static_cast<double>(x);
+  const double r = __builtin_rint(xv * static_cast<double>(f));
+  if constexpr (BITS == 64) {
+    // |r| <= |x| <= 2^63; only x near INT64_MAX can round up to 2^63
+    if (r >= 9223372036854775808.0) return INT64_MAX;
+    return static_cast<int64_t>(r);
+  } else {
+    return static_cast<int32_t>(r);  // |r| <= 2^31, integral
+  }
+}
+
+// Running (M, D, W) of a row folded with one chunk's (mc, dc, wc), mc finite:
+// M' = max(M, mc), D' = rescale(D, 2^(M - M')) + rescale(dc, 2^(mc - M')).
+__device__ __forceinline__ void merge_factors(float M, float mc, float& Mn, float& fa, float& fb) {
+  Mn = fmaxf(M, mc);
+  fa = __builtin_amdgcn_exp2f(M - Mn);  // M = -inf (empty state): 0
+  fb = __builtin_amdgcn_exp2f(mc - Mn);
+}
+
+template <int N, class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+// f(integral_constant<int, i>) for i = 0..N-1, every index a compile-time constant
+template <int N, class F> __device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int DT, int BITS, int DMAX, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   using TR = Traits<DT>;
   using T = typename TR::T;
@@ -167,7 +208,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   __shared__ __align__(16) T Ps[QROWS * VP]; // IO-rounded weights: [row][key]
   __shared__ float red_f[4][QROWS];
   __shared__ AccT red_i[4][QROWS];
-  __shared__ float row_m[QROWS];
   auto vcol = [](int d, int key) -> int {
     if constexpr (DT == FXPR_DTYPE_F32) return key;
     else return key ^ (((d >> 3) & 7) << 3);
@@ -176,8 +216,8 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // The hardware deals consecutive workgroup ids to the 8 XCDs round-robin,
   // so the kv heads of one request (which share every KV page) run at the
-  // same time, one per XCD, and every XCD gets a share of every request:
-  // the XCDs stay balanced whatever the spread of context lengths.
+  // same time on different XCDs, and the XCDs stay balanced whatever the
+  // spread of context lengths.
   const int logical = blockIdx.x;
   const int r = logical / a.num_kv_heads, g = logical % a.num_kv_heads;
   const int qt = blockIdx.y, split = blockIdx.z;
@@ -187,21 +227,24 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   const int ctx = seq_len - q_len;
   const int rows_total = q_len * a.group;
   const int row0 = qt * QROWS;
-  if (row0 >= rows_total || seq_len <= 0) return;  // uniform
+  if (row0 >= rows_total) return;  // uniform
 
-  // Key range of the workgroup (union over its rows), in absolute tiles.
+  // Key range of the workgroup (union over its rows), in absolute tiles, and
+  // the absolute key chunks (CT tiles) it touches. A chunk's statistics are
+  // per row, so they do not depend on the workgroup's other rows.
   const int i_min = row0 / a.group;
   const int i_max = min(rows_total - 1, row0 + QROWS - 1) / a.group;
   const int hi = a.causal ? min(seq_len, ctx + i_max + 1) : seq_len;
   const int lo = a.window > 0 ? max(0, ctx + i_min - a.window + 1) : 0;
   const int t_lo = lo / TILE;
   const int t_hi = hi > lo ? (hi + TILE - 1) / TILE : t_lo;
-  const int ntile = t_hi - t_lo;
-  const int per = a.tiles_per_split > 0 ? a.tiles_per_split : (ntile + a.num_splits - 1) / a.num_splits;
-  constexpr bool PASS2 = MODE == ACCPASS || MODE == ACCCACHED;
-  const int my_lo = (MODE == FUSED) ? t_lo : min(t_hi, t_lo + split * per);
-  const int my_hi = (MODE == FUSED) ? t_hi : min(t_hi, my_lo + per);
-  const bool cached = a.scores != nullptr;
+  const int c_lo = t_lo / CT;
+  int c_hi = t_hi > t_lo ? (t_hi + CT - 1) / CT : c_lo;
+  if constexpr (SPLIT) c_hi = min(c_hi, a.chunk_slots);  // workspace bound (only inconsistent metadata)
+  const int nch = max(0, c_hi - c_lo);
+  const int per = a.chunks_per_split > 0 ? a.chunks_per_split : (nch + a.num_splits - 1) / a.num_splits;
+  const int my_lo = SPLIT ? c_lo + min(nch, split * per) : c_lo;
+  const int my_hi = SPLIT ? min(c_lo + nch, my_lo + per) : c_lo + nch;
 
   const int32_t* bt_row = a.bt + int64_t(r) * a.sbt;
   const T* Kc = static_cast<const T*>(a.k);
@@ -256,6 +299,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     srow[e] = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + 4 * kg + e);
     slope[e] = a.alibi ? a.alibi[srow[e].head] : 0.0f;
   }
+  if (SPLIT && split == 0 && tid < QROWS) {
+    // the chunk range every split of this workgroup's rows covers together
+    const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
+    if (ri.valid) {
+      int* cr = a.crange + 2 * (ri.token * a.num_heads + ri.head);
+      cr[0] = c_lo;
+      cr[1] = c_lo + nch;
+    }
+  }
 
   // K fragments of the lane's key of tile t (key clamped, bt entry given).
   // Every load is issued unconditionally: loads under a branch would leave
@@ -294,115 +346,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     }
   };
 
-  // Cached scores (decode-shaped launches: one 16-row q-tile per (request,
-  // kv head)), written by pass 1 and read back by pass 2 in the MFMA score
-  // layout itself: per (request, kv head, key tile, wave, lane group kg) a
-  // 256-byte block in which lane key k holds its four rows' scores as one
-  // 16-byte vector. Stores and loads are then whole lines; lane groups whose
-  // rows are all outside the q-tile (kg >= score_kg) have no block.
-  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(a.scores, 0, a.score_bytes, kBufferWord3);
-  const uint32_t sc_rg = uint32_t(r * a.num_kv_heads + g) * uint32_t(a.score_tiles);
-  auto sc_off = [&](int t) -> int {  // byte offset of the lane's vector for tile t, or out of range
-    const bool ok = kg < a.score_kg && t < a.score_tiles;
-    const uint32_t blk = ((sc_rg + uint32_t(t)) * 4u + uint32_t(wave)) * uint32_t(a.score_kg) + uint32_t(kg);
-    return ok ? int(blk * 256u + uint32_t(lane & 15) * 16u) : int(0x80000000u);
-  };
-
-  // ---------------- pass 1: row maxima (and cached scores) ----------------
-  float m[4];
-  if constexpr (MODE == FUSED || MODE == MAXPASS) {
-    float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
-    if (my_lo < my_hi) {
-      // Ring of R1 K buffers: tiles t+1 .. t+R1-1 are in flight while tile t
-      // is scored. The page entry of a tile is loaded R1 steps before its K
-      // rows, so waiting for an entry never waits for recent K loads (loads
-      // complete in issue order). Buffers are indexed by compile-time slots
-      // of the R1-times unrolled loop, so no register copy touches a buffer
-      // with loads in flight. The loop body has no branches and issues the
-      // same memory instructions every step, so the compiler can count the
-      // loads in flight exactly: tiles past my_hi are loaded clamped (cache
-      // hits) and scored as fully masked, and the cached-score stores go
-      // through a buffer resource, with an out-of-range offset (dropped by
-      // the hardware) where a lane has nothing to store.
-      constexpr int R1 = 2;
-      KFrag kb[R1][QSTEPS];
-      int eb[R1];
-      auto tl = [&](int x) { return min(x, my_hi - 1); };
-#pragma unroll
-      for (int i = 0; i < R1; ++i) eb[i] = k_entry(tl(my_lo + i));
-#pragma unroll
-      for (int i = 0; i + 1 < R1; ++i) {
-        k_load(tl(my_lo + i), eb[i], kb[i]);
-        eb[i] = k_entry(tl(my_lo + R1 + i));
-      }
-      for (int t = my_lo; t < my_hi; t += R1) {
-#pragma unroll
-        for (int u = 0; u < R1; ++u) {
-          const int sl = (u + R1 - 1) % R1;
-          k_load(tl(t + u + R1 - 1), eb[sl], kb[sl]);
-          eb[sl] = k_entry(tl(t + u + 2 * R1 - 1));
-          const bool live = t + u < my_hi;
-          float s[4];
-          k_scores(t + u, kb[u], s);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            s[e] = live ? s[e] : -__builtin_inff();
-            mx[e] = fmaxf(mx[e], s[e]);
-          }
-          if (MODE == MAXPASS && cached) {
-            const u32x4 v = {__builtin_bit_cast(uint32_t, s[0]), __builtin_bit_cast(uint32_t, s[1]),
-                             __builtin_bit_cast(uint32_t, s[2]), __builtin_bit_cast(uint32_t, s[3])};
-            __builtin_amdgcn_raw_buffer_store_b128(v, srsrc, live ? sc_off(t + u) : int(0x80000000u), 0, 0);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o, 64));
-      if ((lane & 15) == 0) red_f[wave][4 * kg + e] = mx[e];
-    }
-    __syncthreads();
-    if constexpr (MODE == MAXPASS) {
-      if (tid < QROWS) {
-        const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
-        const float v = fmaxf(fmaxf(red_f[0][tid], red_f[1][tid]), fmaxf(red_f[2][tid], red_f[3][tid]));
-        if (ri.valid) a.pmax[(ri.token * a.num_heads + ri.head) * a.num_splits + split] = v;
-      }
-      return;
-    }
-    if (tid < QROWS) {
-      const float v = fmaxf(fmaxf(red_f[0][tid], red_f[1][tid]), fmaxf(red_f[2][tid], red_f[3][tid]));
-      row_m[tid] = v;
-    }
-  } else {  // pass 2 only: fold the per-split maxima
-    if (tid < QROWS) {
-      const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
-      float v = -__builtin_inff();
-      if (ri.valid) {
-        const float* pm = a.pmax + (ri.token * a.num_heads + ri.head) * a.num_splits;
-        for (int s2 = 0; s2 < a.num_splits; ++s2) v = fmaxf(v, pm[s2]);
-      }
-      row_m[tid] = v;
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float v = row_m[4 * kg + e];
-    m[e] = (srow[e].valid && v != -__builtin_inff()) ? v : 0.0f;  // no key: pin to 0
-  }
-
-  // ---------------- pass 2: integer denominators and weighted V ----------------
-  AccT den[4] = {0, 0, 0, 0};
-  AccT wv[DB_PER_WAVE][4];
-#pragma unroll
-  for (int b = 0; b < DB_PER_WAVE; ++b)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) wv[b][e] = 0;
-
-  constexpr bool from_cache = MODE == ACCCACHED;
   // V chunk c = i*256 + tid of a tile: key c / VCH, d chunk (c % VCH) * CH
   // (each wave instruction reads whole 16-byte-aligned key rows).
   auto v_entries = [&](int t, int (&ve)[VITER]) {
@@ -421,18 +364,12 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
                                               (d0 < a.head_dim ? d0 : 0));
     }
   };
-  auto s_load = [&](int t, float (&s)[4]) {
-    const int key = t * TILE + wave * 16 + (lane & 15);
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(srsrc, sc_off(t), 0, 0);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // element copied out first: __builtin_bit_cast of a vector element
-      // lvalue reads the vector's first element whatever the index
-      const uint32_t x = v[e];
-      s[e] = (srow[e].valid && key >= srow[e].kstart && key < srow[e].kend) ? __builtin_bit_cast(float, x)
-                                                                             : -__builtin_inff();
-    }
-  };
+
+  // Chunk accumulators (lane rows 4*kg + e; PV layout d = db*16 + lane%16)
+  // and the row maxima the chunk's weights are taken against.
+  float m[4];
+  AccT den[4];
+  AccT wv[DB_PER_WAVE][4];
 
   // One key tile: weights from the scores, V tile to LDS, PV partials.
   auto accumulate = [&](int t, const u32x4 (&vr)[VITER], const float (&s)[4]) __attribute__((always_inline)) {
@@ -502,89 +439,165 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     __syncthreads();
   };
 
+  // Running state of the lane's rows (single-pass launches only).
+  float Mr[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  AccT Dr[4] = {0, 0, 0, 0};
+  AccT Wr[DB_PER_WAVE][4];
+#pragma unroll
+  for (int b = 0; b < DB_PER_WAVE; ++b)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Wr[b][e] = 0;
+
   if (my_lo < my_hi) {
-    // Ring of R2 slots (V chunks and their page entries, plus the cached
-    // scores or the K fragments and their entries), scheduled as the pass-1
-    // ring: entries R2 steps ahead of their loads, compile-time slots.
-    constexpr int R2 = MODE == ACCCACHED ? 3 : 2;
-    u32x4 vb[R2][VITER];
-    int veb[R2][VITER];
-    float sb[R2][4];
-    KFrag kb[R2][QSTEPS];
-    int keb[R2];
-    auto tl = [&](int x) { return min(x, my_hi - 1); };
-    auto entries = [&](int x, int (&ve)[VITER], int& ke) {
-      v_entries(tl(x), ve);
-      if constexpr (!from_cache) ke = k_entry(tl(x));
+    // One chunk is 2*CT pipeline steps: CT K tiles (scores into registers,
+    // then the chunk's row maxima), then the same CT tiles of V (weights
+    // against those maxima, integer partials). Loads run R-1 steps ahead of
+    // use and page entries R steps ahead of their loads, straight across the
+    // K -> V boundary and into the next chunk, so the maxima reduction and
+    // the chunk's fold overlap loads in flight. Buffers are indexed by
+    // compile-time slots, every load is issued unconditionally (tiles outside
+    // the chunk's live range, or past the last chunk, reload a live tile),
+    // and only the arithmetic of dead tiles is skipped (uniformly).
+    constexpr int R = 2;
+    constexpr int NSTEP = 2 * CT;
+    static_assert(CT % R == 0, "ring slots must repeat every chunk");
+    KFrag kb[R][QSTEPS];
+    int eb[R];
+    u32x4 vb[R][VITER];
+    int veb[R][VITER];
+    float sc[CT][4];
+
+    int c = my_lo;
+    auto live_lo = [&](int cc) { return max(cc * CT, t_lo); };
+    auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
+    int ta = live_lo(c), te = live_hi(c);
+    int nc = c + 1 < my_hi ? c + 1 : c;
+    int nta = live_lo(nc), nte = live_hi(nc);
+    // step j of the current chunk (j < NSTEP) or of the next (j >= NSTEP)
+    auto entry_step = [&](auto J) __attribute__((always_inline)) {
+      constexpr int j = decltype(J)::value, jj = j % NSTEP, sl = j % R;
+      const int base = (j >= NSTEP ? nc : c) * CT, l0 = j >= NSTEP ? nta : ta, l1 = j >= NSTEP ? nte : te;
+      const int t = min(max(base + (jj < CT ? jj : jj - CT), l0), l1 - 1);
+      if constexpr (jj < CT) eb[sl] = k_entry(t);
+      else v_entries(t, veb[sl]);
     };
-    auto loads = [&](int x, const int (&ve)[VITER], u32x4 (&vr)[VITER], float (&sc)[4], int ke,
-                     KFrag (&kf)[QSTEPS]) {
-      v_load(tl(x), ve, vr);
-      if constexpr (from_cache) s_load(tl(x), sc);
-      else k_load(tl(x), ke, kf);
+    auto load_step = [&](auto J) __attribute__((always_inline)) {
+      constexpr int j = decltype(J)::value, jj = j % NSTEP, sl = j % R;
+      const int base = (j >= NSTEP ? nc : c) * CT, l0 = j >= NSTEP ? nta : ta, l1 = j >= NSTEP ? nte : te;
+      const int t = min(max(base + (jj < CT ? jj : jj - CT), l0), l1 - 1);
+      if constexpr (jj < CT) k_load(t, eb[sl], kb[sl]);
+      else v_load(t, veb[sl], vb[sl]);
     };
+    static_for<R>([&](auto I) { entry_step(I); });
+    static_for<R - 1>([&](auto I) {
+      load_step(I);
+      entry_step(std::integral_constant<int, decltype(I)::value + R>{});
+    });
+
+    for (;;) {
+      float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+      float mc[4];
 #pragma unroll
-    for (int i = 0; i < R2; ++i) entries(my_lo + i, veb[i], keb[i]);
+      for (int e = 0; e < 4; ++e) den[e] = 0;
 #pragma unroll
-    for (int i = 0; i + 1 < R2; ++i) {
-      loads(my_lo + i, veb[i], vb[i], sb[i], keb[i], kb[i]);
-      entries(my_lo + R2 + i, veb[i], keb[i]);
-    }
-    for (int t = my_lo; t < my_hi; t += R2) {
+      for (int b = 0; b < DB_PER_WAVE; ++b)
 #pragma unroll
-      for (int u = 0; u < R2; ++u) {
-        const int sl = (u + R2 - 1) % R2;
-        loads(t + u + R2 - 1, veb[sl], vb[sl], sb[sl], keb[sl], kb[sl]);
-        entries(t + u + 2 * R2 - 1, veb[sl], keb[sl]);
-        if (t + u < my_hi) {
-          if constexpr (from_cache) {
-            accumulate(t + u, vb[u], sb[u]);
+        for (int e = 0; e < 4; ++e) wv[b][e] = 0;
+
+      static_for<NSTEP>([&](auto I) __attribute__((always_inline)) {
+        constexpr int i = decltype(I)::value, sl = i % R;
+        load_step(std::integral_constant<int, i + R - 1>{});
+        entry_step(std::integral_constant<int, i + 2 * R - 1>{});
+        if constexpr (i < CT) {
+          const int t = c * CT + i;
+          if (t >= ta && t < te) {
+            k_scores(t, kb[sl], sc[i]);
           } else {
-            float s[4];
-            k_scores(t + u, kb[u], s);
-            accumulate(t + u, vb[u], s);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[i][e] = -__builtin_inff();
           }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], sc[i][e]);
+          if constexpr (i == CT - 1) {
+            // the chunk's row maxima: 16 key lanes, then the 4 waves
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma unroll
+              for (int o = 1; o < 16; o <<= 1) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o, 64));
+              if ((lane & 15) == 0) red_f[wave][4 * kg + e] = mx[e];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int row = 4 * kg + e;
+              mc[e] = fmaxf(fmaxf(red_f[0][row], red_f[1][row]), fmaxf(red_f[2][row], red_f[3][row]));
+              m[e] = (srow[e].valid && mc[e] != -__builtin_inff()) ? mc[e] : 0.0f;  // no key: pin to 0
+            }
+          }
+        } else {
+          const int t = c * CT + (i - CT);
+          if (t >= ta && t < te) accumulate(t, vb[sl], sc[i - CT]);
         }
-      }
-    }
-  }
+      });
 
-  // denominators: sum over the 16 key lanes, then over the waves
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
-    if ((lane & 15) == 0) red_i[wave][4 * kg + e] = den[e];
-  }
-  __syncthreads();
-
-  // PV layout: lane holds rows 4*kg + e, d = db*16 + lane%16
-  if (PASS2 && a.num_splits > 1) {
-    if (tid < QROWS) {
-      const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
-      AccT dsum = wadd<BITS>(wadd<BITS>(red_i[0][tid], red_i[1][tid]), wadd<BITS>(red_i[2][tid], red_i[3][tid]));
-      if (ri.valid) static_cast<AccT*>(a.den_ws)[(ri.token * a.num_heads + ri.head) * a.num_splits + split] = dsum;
-    }
-#pragma unroll
-    for (int b = 0; b < DB_PER_WAVE; ++b) {
-      const int d = (wave + 4 * b) * 16 + (lane & 15);
-      if (wave + 4 * b >= DBLK || d >= a.head_dim) continue;
+      // the chunk's denominators: 16 key lanes, then the 4 waves
+      AccT dc[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        if (!srow[e].valid) continue;
-        AccT* dst = static_cast<AccT*>(a.wv_ws) +
-                    ((srow[e].token * a.num_heads + srow[e].head) * a.num_splits + split) * a.head_dim + d;
-        *dst = wv[b][e];
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
+        if ((lane & 15) == 0) red_i[wave][4 * kg + e] = den[e];
       }
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 4 * kg + e;
+        dc[e] = wadd<BITS>(wadd<BITS>(red_i[0][row], red_i[1][row]), wadd<BITS>(red_i[2][row], red_i[3][row]));
+      }
+
+      if constexpr (SPLIT) {
+        // the chunk's partials, per row: maximum, denominator, weighted V
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (!srow[e].valid) continue;
+          const int64_t slot = (srow[e].token * a.num_heads + srow[e].head) * a.chunk_slots + c;
+          if ((lane & 15) == 0 && wave == 0) {
+            a.pmax[slot] = mc[e];
+            static_cast<AccT*>(a.den_ws)[slot] = dc[e];
+          }
+#pragma unroll
+          for (int b = 0; b < DB_PER_WAVE; ++b) {
+            const int d = (wave + 4 * b) * 16 + (lane & 15);
+            if (wave + 4 * b < DBLK && d < a.head_dim) static_cast<AccT*>(a.wv_ws)[slot * a.head_dim + d] = wv[b][e];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (mc[e] == -__builtin_inff()) continue;  // no key of the row in this chunk
+          float Mn, fa, fb;
+          merge_factors(Mr[e], mc[e], Mn, fa, fb);
+          Dr[e] = wadd<BITS>(rescale<BITS>(Dr[e], fa), rescale<BITS>(dc[e], fb));
+#pragma unroll
+          for (int b = 0; b < DB_PER_WAVE; ++b)
+            Wr[b][e] = wadd<BITS>(rescale<BITS>(Wr[b][e], fa), rescale<BITS>(wv[b][e], fb));
+          Mr[e] = Mn;
+        }
+      }
+
+      if (++c >= my_hi) break;
+      ta = nta;
+      te = nte;
+      nc = c + 1 < my_hi ? c + 1 : c;
+      nta = live_lo(nc);
+      nte = live_hi(nc);
     }
-  } else {  // single split: finish here
+  }
+
+  if constexpr (!SPLIT) {
     float den_f[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = 4 * kg + e;
-      const AccT dsum = wadd<BITS>(wadd<BITS>(red_i[0][row], red_i[1][row]), wadd<BITS>(red_i[2][row], red_i[3][row]));
-      den_f[e] = fmaxf(acc_f32<BITS>(dsum, a.fxp_inv), 1.0e-6f);
-    }
+    for (int e = 0; e < 4; ++e) den_f[e] = fmaxf(acc_f32<BITS>(Dr[e], a.fxp_inv), 1.0e-6f);
     T* Op = static_cast<T*>(a.o);
 #pragma unroll
     for (int b = 0; b < DB_PER_WAVE; ++b) {
@@ -593,14 +606,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if (!srow[e].valid) continue;
-        const float num = acc_f32<BITS>(wv[b][e], a.fxp_inv);
+        const float num = acc_f32<BITS>(Wr[b][e], a.fxp_inv);
         Op[srow[e].token * a.so_t + int64_t(srow[e].head) * a.so_h + d] = Io<DT>::store(div_rn(num, den_f[e]));
       }
     }
   }
 }
 
-// Sum the per-split integer partials of each (token, head) and divide.
+// Fold the per-chunk partials of each (token, head) in ascending chunk order
+// (the kernel's single-pass fold, step for step) and divide.
 template <int DT, int BITS>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t num_tokens) {
   using T = typename Traits<DT>::T;
@@ -613,34 +627,36 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t n
   if (idx >= total) return;
   const int d = int(idx % a.head_dim);
   const int64_t th = idx / a.head_dim;  // token * Hq + head
-  const AccT* den = static_cast<const AccT*>(a.den_ws) + th * a.num_splits;
-  const AccT* wv = static_cast<const AccT*>(a.wv_ws) + th * a.num_splits * a.head_dim + d;
-  AccT ds = 0, ws = 0;
-  for (int s = 0; s < a.num_splits; ++s) {
-    ds = wadd<BITS>(ds, den[s]);
-    ws = wadd<BITS>(ws, wv[int64_t(s) * a.head_dim]);
+  const int c0 = max(0, a.crange[2 * th]), c1 = min(a.chunk_slots, a.crange[2 * th + 1]);
+  float M = -__builtin_inff();
+  AccT D = 0, W = 0;
+  for (int c = c0; c < c1; ++c) {
+    const int64_t slot = th * a.chunk_slots + c;
+    const float mc = a.pmax[slot];
+    if (mc == -__builtin_inff()) continue;
+    float Mn, fa, fb;
+    merge_factors(M, mc, Mn, fa, fb);
+    D = wadd<BITS>(rescale<BITS>(D, fa), rescale<BITS>(static_cast<const AccT*>(a.den_ws)[slot], fb));
+    W = wadd<BITS>(rescale<BITS>(W, fa), rescale<BITS>(static_cast<const AccT*>(a.wv_ws)[slot * a.head_dim + d], fb));
+    M = Mn;
   }
-  const float den_f = fmaxf(acc_f32<BITS>(ds, a.fxp_inv), 1.0e-6f);
+  const float den_f = fmaxf(acc_f32<BITS>(D, a.fxp_inv), 1.0e-6f);
   const int64_t token = th / a.num_heads;
   const int head = int(th % a.num_heads);
   static_cast<T*>(a.o)[token * a.so_t + int64_t(head) * a.so_h + d] =
-      Io<DT>::store(div_rn(acc_f32<BITS>(ws, a.fxp_inv), den_f));
+      Io<DT>::store(div_rn(acc_f32<BITS>(W, a.fxp_inv), den_f));
 }
 
 template <int DT, int BITS, int DMAX>
 int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st) {
   dim3 grid(unsigned(num_requests * a.num_kv_heads), unsigned(max_qtiles), unsigned(a.num_splits));
-  if (a.num_splits <= 1 && a.scores == nullptr) {
-    attn_kernel<DT, BITS, DMAX, FUSED><<<grid, kThreads, 0, st>>>(a);
+  if (a.num_splits <= 1) {
+    attn_kernel<DT, BITS, DMAX, false><<<grid, kThreads, 0, st>>>(a);
     return launch_status();
   }
-  attn_kernel<DT, BITS, DMAX, MAXPASS><<<grid, kThreads, 0, st>>>(a);
-  if (a.scores) attn_kernel<DT, BITS, DMAX, ACCCACHED><<<grid, kThreads, 0, st>>>(a);
-  else attn_kernel<DT, BITS, DMAX, ACCPASS><<<grid, kThreads, 0, st>>>(a);
-  if (a.num_splits > 1) {
-    const int64_t total = num_tokens * a.num_heads * a.head_dim;
-    attn_combine_kernel<DT, BITS><<<dim3(unsigned(cdiv(total, 256))), 256, 0, st>>>(a, num_tokens);
-  }
+  attn_kernel<DT, BITS, DMAX, true><<<grid, kThreads, 0, st>>>(a);
+  const int64_t total = num_tokens * a.num_heads * a.head_dim;
+  attn_combine_kernel<DT, BITS><<<dim3(unsigned(cdiv(total, 256))), 256, 0, st>>>(a, num_tokens);
   return launch_status();
 }
 
