@@ -55,7 +55,7 @@ WsLayout ws_layout(int64_t num_tokens, int num_heads, int head_dim, int int_bits
 // (requests shorter than the longest get empty splits). Split counts never
 // change bits.
 namespace {
-constexpr int kSplitChunks = 2;
+constexpr int kSplitChunks = 1;
 
 struct SplitPlan {
   int splits, chunks_per_split;

@@ -630,15 +630,31 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t n
   const int c0 = max(0, a.crange[2 * th]), c1 = min(a.chunk_slots, a.crange[2 * th + 1]);
   float M = -__builtin_inff();
   AccT D = 0, W = 0;
-  for (int c = c0; c < c1; ++c) {
-    const int64_t slot = th * a.chunk_slots + c;
-    const float mc = a.pmax[slot];
-    if (mc == -__builtin_inff()) continue;
-    float Mn, fa, fb;
-    merge_factors(M, mc, Mn, fa, fb);
-    D = wadd<BITS>(rescale<BITS>(D, fa), rescale<BITS>(static_cast<const AccT*>(a.den_ws)[slot], fb));
-    W = wadd<BITS>(rescale<BITS>(W, fa), rescale<BITS>(static_cast<const AccT*>(a.wv_ws)[slot * a.head_dim + d], fb));
-    M = Mn;
+  // batches of NB chunks: every load of a batch is issued (clamped to the
+  // range) before the sequential fold, so the loads overlap
+  constexpr int NB = 8;
+  const AccT* den_p = static_cast<const AccT*>(a.den_ws) + th * a.chunk_slots;
+  const AccT* wv_p = static_cast<const AccT*>(a.wv_ws) + th * a.chunk_slots * a.head_dim + d;
+  const float* pm_p = a.pmax + th * a.chunk_slots;
+  for (int cb = c0; cb < c1; cb += NB) {
+    float mc[NB];
+    AccT dc[NB], wc[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int c = min(cb + k, c1 - 1);
+      mc[k] = pm_p[c];
+      dc[k] = den_p[c];
+      wc[k] = wv_p[int64_t(c) * a.head_dim];
+    }
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      if (cb + k >= c1 || mc[k] == -__builtin_inff()) continue;
+      float Mn, fa, fb;
+      merge_factors(M, mc[k], Mn, fa, fb);
+      D = wadd<BITS>(rescale<BITS>(D, fa), rescale<BITS>(dc[k], fb));
+      W = wadd<BITS>(rescale<BITS>(W, fa), rescale<BITS>(wc[k], fb));
+      M = Mn;
+    }
   }
   const float den_f = fmaxf(acc_f32<BITS>(D, a.fxp_inv), 1.0e-6f);
   const int64_t token = th / a.num_heads;
