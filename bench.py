@@ -253,6 +253,36 @@ def wl_decode(steps, warmup, splits=0, int_bits=32, frac_bits=16, B=64, hq=32, h
             "ms": round(ms, 5), "bytes": nbytes, "splits": s_eff, "roofline": hbm_roofline(nbytes, ms)}
 
 
+def wl_prefill(steps, warmup, splits=0, int_bits=32, frac_bits=16, B=4, L=2048, hq=32, hkv=8, d=128, ps=16,
+               seed=0):
+    """Paged causal prefill attention: B prompts of L new tokens each (no
+    cached context), Llama-3-8B head shape, bf16, pages of one shuffled pool.
+    Algorithmic flops = 4 * Hq * D * sum over rows of the keys it attends
+    (QK^T and PV, 2 flops per multiply-add), against the bf16 MFMA peak."""
+    import torch
+
+    g = torch.Generator("cpu").manual_seed(seed)
+    nb = B * (L // ps)
+    bt = torch.randperm(nb, generator=g).to(torch.int32).reshape(B, L // ps)
+    q = torch.randn(B * L, hq, d, generator=g).to(torch.bfloat16).to("cuda")
+    kv = torch.randn(nb, 2, ps, hkv, d, generator=g).to(torch.bfloat16).to("cuda")
+    qsl = (torch.arange(B + 1, dtype=torch.int32) * L).to("cuda")
+    sl = torch.full((B,), L, dtype=torch.int32, device="cuda")
+    bt_d = bt.to("cuda")
+    o = torch.empty_like(q)
+    scale = 1.0 / d ** 0.5
+
+    def fn():
+        torch.ops.fxpr.unified_attention_fxp(q, kv, o, qsl, sl, bt_d, L, None, True, scale,
+                                             int_bits, frac_bits, 0.0, 0, splits)
+
+    ms = time_op(fn, [()], steps, warmup)
+    flops = 4 * hq * d * B * (L * (L + 1) // 2)
+    return {"workload": f"prefill attn bf16 causal B={B} L={L} Hq={hq} Hkv={hkv} d={d} page {ps} "
+                        f"Q{frac_bits}/i{int_bits}",
+            "ms": round(ms, 5), "flops": flops, "roofline": mfma_roofline(flops, ms, BF16_PEAK_TFLOPS)}
+
+
 def wl_hbm_copy(steps, warmup, nbytes=1 << 30):
     """torch copy_ of a known size: the reference point for HBM bandwidth and
     for scaling the FETCH_SIZE / WRITE_SIZE counters."""
@@ -272,6 +302,7 @@ WORKLOADS = {
     "decode_attn_s4": lambda s, w: wl_decode(s, w, 4),
     "decode_attn_s8": lambda s, w: wl_decode(s, w, 8),
     "decode_attn_s16": lambda s, w: wl_decode(s, w, 16),
+    "prefill_attn": lambda s, w: wl_prefill(s, w),
     "gemm_lm_head": lambda s, w: wl_gemm(s, w, 8192),
     "gemm_lm_head_m2048": lambda s, w: wl_gemm(s, w, 2048),
     "gemm_lm_head_m256": lambda s, w: wl_gemm(s, w, 256),
