@@ -144,7 +144,11 @@ int64_t fxpr_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k,
 
 /*
  * Unified paged prefill + decode attention with fixed-point cross-tile
- * reductions. q [num_tokens, num_heads, head_dim] and o share io_dtype
+ * reductions: one pass over K and V, softmax statistics per 512-key chunk
+ * (each chunk's weights against its own row maximum), chunks folded in
+ * ascending order in fixed point; a row whose keys fit in one chunk gets
+ * the reference's formula exactly, longer rows agree with it within the
+ * fixed-point tolerance. q [num_tokens, num_heads, head_dim] and o share io_dtype
  * (bf16 / f16 / f32) with the caches; k_cache / v_cache are the two halves
  * of a vLLM [num_blocks, 2, page_size, num_kv_heads, head_dim] cache (any
  * strides, unit stride along head_dim). Metadata: query_start_loc
@@ -153,7 +157,8 @@ int64_t fxpr_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k,
  * log2 units. softmax_scale_log2 = scale * log2(e); softcap_log2 =
  * logit_softcap * log2(e) (0 = off); window_size 0 = off. num_kv_splits:
  * 0 = automatic (fxpr_attention_splits() reports the choice), >= 1 = that
- * many KV splits. The launch needs a workspace of
+ * many KV splits (a launch whose split partials would exceed 1 GiB runs
+ * unsplit; the bits are the same). The launch needs a workspace of
  * fxpr_attention_workspace_bytes() bytes when that is non-zero (no zeroing).
  * The output is bitwise independent of num_splits, of the batch the request
  * is in and of max_query_len.
@@ -182,10 +187,9 @@ int fxpr_attention_splits(int num_requests, int num_kv_heads, int group,
                           int page_size, int requested);
 
 /* Workspace bytes fxpr_unified_attention needs for this launch (0 = none):
- * per-split maxima and integer partials when num_splits > 1, plus a cache of
- * the pass-1 scores for decode-shaped launches (max_query_len * group <= 16)
- * so pass 2 does not re-read K. Replaces the per-call scratch of
- * attention.py:839-851. */
+ * with more than one split, per (token, head) the chunk range and per
+ * (token, head, chunk) the maximum, the integer denominator and the integer
+ * weighted-V row. Replaces the per-call scratch of attention.py:839-851. */
 int64_t fxpr_attention_workspace_bytes(int num_requests, int64_t num_tokens,
                                        int num_heads, int num_kv_heads,
                                        int head_dim, int int_bits,
