@@ -613,6 +613,315 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   }
 }
 
+// Prefill-shaped launches (16-bit inputs, one split): 64 query rows per
+// workgroup, each wave owning 16 of them, so a key tile staged in LDS serves
+// four times the rows of attn_kernel's 16-row tile. A chunk's scores are not
+// kept: its K tiles are read twice, once for the chunk's row maxima and again
+// (with the V tiles) for the weights. Every row gets attn_kernel's bits: the
+// same MFMA chains per score and per weighted-V element (rows of one MFMA are
+// independent), the same chunk statistics (keys a row cannot see contribute
+// exact zeros, so the workgroup's wider key range changes nothing) and the
+// same fold.
+constexpr int PQ_WAVES = 8;
+constexpr int PQROWS = 16 * PQ_WAVES;
+constexpr int kPThreads = 64 * PQ_WAVES;
+
+template <int DT, int BITS, int DMAX>
+__global__ __launch_bounds__(kPThreads, 2) void attn_prefill_kernel(AttnArgs a) {
+  static_assert(DT != FXPR_DTYPE_F32, "16-bit inputs only");
+  using TR = Traits<DT>;
+  using T = typename TR::T;
+  using AccT = typename AccOf<BITS>::T;
+  constexpr int KI = TR::KI, CH = TR::CH, QUNIT = TR::QUNIT;
+  constexpr int QSTEPS = DMAX / KI;
+  constexpr int DBLK = DMAX / 16;
+  constexpr int VP = TILE + 8;
+  constexpr int VNP = DMAX + 16;
+  constexpr int VCH = DMAX / CH;
+  constexpr int VITER = TILE * VCH / kPThreads;
+  constexpr int KCPR = DMAX / CH;
+  // K tile [key][d], 16-byte chunk c of key row r at slot c ^ kswz(r): a
+  // fragment read (16 consecutive rows, one chunk each) hits distinct banks.
+  __shared__ __align__(16) T Kt[2][TILE * DMAX];
+  __shared__ __align__(16) T Vt[2][TILE * VNP];
+  __shared__ __align__(16) T Ps[PQ_WAVES][16 * VP];  // each wave's weights, [row][key]
+  auto kswz = [](int r) -> int {
+    if constexpr (KCPR >= 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else return (r >> 1) & 7;
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, kg = lane >> 4;
+  const int r = blockIdx.x / a.num_kv_heads, g = blockIdx.x % a.num_kv_heads;
+  const int q_start = a.qsl[r];
+  const int q_len = a.qsl[r + 1] - q_start;
+  const int seq_len = a.seq_lens[r];
+  const int ctx = seq_len - q_len;
+  const int rows_total = q_len * a.group;
+  const int row0 = blockIdx.y * PQROWS;
+  if (row0 >= rows_total) return;  // uniform
+  const int wrow0 = row0 + 16 * wave;
+
+  const int i_min = row0 / a.group;
+  const int i_max = min(rows_total - 1, row0 + PQROWS - 1) / a.group;
+  const int hi = a.causal ? min(seq_len, ctx + i_max + 1) : seq_len;
+  const int lo = a.window > 0 ? max(0, ctx + i_min - a.window + 1) : 0;
+  const int t_lo = lo / TILE;
+  const int t_hi = hi > lo ? (hi + TILE - 1) / TILE : t_lo;
+  const int c_lo = t_lo / CT;
+  const int c_hi = t_hi > t_lo ? (t_hi + CT - 1) / CT : c_lo;
+
+  const int32_t* bt_row = a.bt + int64_t(r) * a.sbt;
+  const T* Kc = static_cast<const T*>(a.k);
+  const T* Vc = static_cast<const T*>(a.v);
+  const T* Qp = static_cast<const T*>(a.q);
+  auto clamp_key = [&](int key) { return max(0, min(key, seq_len - 1)); };
+  auto bt_entry = [&](int key) -> int {
+    const int lb = a.ps_shift >= 0 ? (key >> a.ps_shift) : key / a.page_size;
+    return bt_row[min(lb, a.max_blocks - 1)];
+  };
+  const int last_block = int(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
+  auto row_addr = [&](int key, int entry, int64_t sb, int64_t ss, int64_t sh) -> uint64_t {
+    const uint32_t p = uint32_t(entry < 0 ? 0 : min(entry, last_block));
+    const uint32_t slot = uint32_t(a.ps_shift >= 0 ? (key & (a.page_size - 1)) : key % a.page_size);
+    return uint64_t(p) * uint32_t(sb) + uint64_t(slot) * uint32_t(ss) + uint64_t(uint32_t(g)) * uint32_t(sh);
+  };
+
+  // Q fragments of the wave's rows (MFMA A operand: row lane%16, k slots kg).
+  u32x4 qf[QSTEPS];
+  {
+    const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + (lane & 15));
+    const T* qbase = Qp + qrow.token * a.sq_t + int64_t(qrow.head) * a.sq_h;
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) {
+      const int d = 32 * j + 8 * kg;
+      qf[j] = (qrow.valid && d < a.head_dim) ? *reinterpret_cast<const u32x4*>(qbase + d) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // Rows of the score / PV layout: the wave's rows 4*kg + e, as their valid
+  // key ranges (empty for rows outside the request) and query positions.
+  int ks[4], ke[4], qp[4];
+  float slope[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + 4 * kg + e);
+    ks[e] = ri.valid ? ri.kstart : 0x7fffffff;
+    ke[e] = ri.valid ? ri.kend : 0;
+    qp[e] = ri.qpos;
+    slope[e] = a.alibi ? a.alibi[ri.head] : 0.0f;
+  }
+
+  // Whole key rows per instruction: chunk c = i*256 + tid of a tile is key
+  // c / VCH, d chunk c % VCH. Loads are unconditional (keys clamped).
+  // K and V rows of one key share its page entry: entries first, then loads.
+  auto tile_entries = [&](int t, int (&ve)[VITER]) {
+#pragma unroll
+    for (int i = 0; i < VITER; ++i) ve[i] = bt_entry(clamp_key(t * TILE + (i * kPThreads + tid) / VCH));
+  };
+  auto tile_load = [&](const T* base, int64_t sb, int64_t ss, int64_t sh, int t, const int (&ve)[VITER],
+                       u32x4 (&vr)[VITER]) {
+#pragma unroll
+    for (int i = 0; i < VITER; ++i) {
+      const int c = i * kPThreads + tid;
+      const int key = clamp_key(t * TILE + c / VCH), d0 = (c % VCH) * CH;
+      vr[i] = *reinterpret_cast<const u32x4*>(base + row_addr(key, ve[i], sb, ss, sh) + (d0 < a.head_dim ? d0 : 0));
+    }
+  };
+  auto k_store = [&](int buf, const u32x4 (&vr)[VITER]) {
+#pragma unroll
+    for (int i = 0; i < VITER; ++i) {
+      const int c = i * kPThreads + tid;
+      const int rr = c / VCH, cc = c % VCH;
+      *reinterpret_cast<u32x4*>(&Kt[buf][rr * DMAX + (cc ^ kswz(rr)) * CH]) = vr[i];
+    }
+  };
+  auto v_store = [&](int buf, const u32x4 (&vr)[VITER]) {
+#pragma unroll
+    for (int i = 0; i < VITER; ++i) {
+      const int c = i * kPThreads + tid;
+      *reinterpret_cast<u32x4*>(&Vt[buf][(c / VCH) * VNP + (c % VCH) * CH]) = vr[i];
+    }
+  };
+  // Scores of key block kb (16 keys) of tile t for the lane's rows.
+  auto block_scores = [&](int buf, int t, int kb, float (&s)[4]) {
+    const int rr = kb * 16 + (lane & 15);
+    const T* row = &Kt[buf][rr * DMAX];
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j)
+      acc = TR::mma(qf[j], *reinterpret_cast<const u32x4*>(row + ((4 * j + kg) ^ kswz(rr)) * CH), acc);
+    const int key = t * TILE + rr;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = __fmul_rn(acc[e], a.scale_log2);
+      if (a.softcap_log2 > 0.0f) x = a.softcap_log2 * tanh_approx(x / a.softcap_log2);
+      if (a.alibi) x = x + slope[e] * static_cast<float>(key - qp[e]);
+      s[e] = (key >= ks[e] && key < ke[e]) ? x : -__builtin_inff();
+    }
+  };
+
+  float mx[4], m[4];
+  AccT den[4];
+  AccT wv[DBLK][4];
+  float Mr[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  AccT Dr[4] = {0, 0, 0, 0};
+  AccT Wr[DBLK][4];
+#pragma unroll
+  for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Wr[b][e] = 0;
+  auto reset = [&]() {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      mx[e] = -__builtin_inff();
+      den[e] = 0;
+    }
+#pragma unroll
+    for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv[b][e] = 0;
+  };
+
+  // Steps: per chunk, phase A over its live tiles (K), then phase B over the
+  // same tiles (K and V). Each step's tiles were loaded into registers during
+  // the previous step; they are written to an LDS buffer (alternating), then
+  // the next step's loads are issued and one barrier separates the writes
+  // from the reads (a buffer is rewritten two steps after it was read).
+  if (c_lo < c_hi) {
+    u32x4 kr[VITER], vr[VITER];
+    int c = c_lo, phase = 0, t = max(c * CT, t_lo);
+    int ve[VITER];
+    auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
+    tile_entries(t, ve);
+    tile_load(Kc, a.sk_b, a.sk_s, a.sk_h, t, ve, kr);
+    reset();
+    int buf = 0;
+    for (;;) {
+      const int te = live_hi(c);
+      k_store(buf, kr);
+      if (phase == 1) v_store(buf, vr);
+      // the next step
+      int nc = c, nphase = phase, nt = t + 1;
+      if (nt >= te) {
+        if (phase == 0) {
+          nphase = 1;
+          nt = max(c * CT, t_lo);
+        } else {
+          nc = c + 1;
+          nphase = 0;
+          nt = max(nc * CT, t_lo);
+        }
+      }
+      const bool more = nc < c_hi;
+      if (more) {
+        tile_entries(nt, ve);
+        tile_load(Kc, a.sk_b, a.sk_s, a.sk_h, nt, ve, kr);
+        if (nphase == 1) tile_load(Vc, a.sv_b, a.sv_s, a.sv_h, nt, ve, vr);
+      }
+      __syncthreads();
+
+      if (phase == 0) {
+#pragma unroll
+        for (int kb = 0; kb < TILE / 16; ++kb) {
+          float s[4];
+          block_scores(buf, t, kb, s);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], s[e]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (nphase == 1 && nc == c) {  // the chunk's row maxima over its 16 key lanes
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o, 64));
+            m[e] = mx[e] != -__builtin_inff() ? mx[e] : 0.0f;  // no key: pin to 0
+          }
+        }
+      } else {
+        T* Pw = Ps[wave];
+#pragma unroll
+        for (int kb = 0; kb < TILE / 16; ++kb) {
+          float s[4];
+          block_scores(buf, t, kb, s);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float w = __builtin_amdgcn_exp2f(s[e] - m[e]);
+            den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
+            Pw[(4 * kg + e) * VP + kb * 16 + (lane & 15)] = Io<DT>::store(w);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // Pw is the wave's own: its writes complete before its reads.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const T* Vb = Vt[buf];
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) {
+#pragma unroll
+          for (int u0 = 0; u0 < TILE; u0 += QUNIT) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k0 = 0; k0 < QUNIT; k0 += KI) {
+              const int key = u0 + k0 + 8 * kg;
+              const int j = lane & 15;
+              typedef short v4s __attribute__((ext_vector_type(4)));
+              const T* src = &Vb[(key + (j >> 2)) * VNP + db * 16 + 4 * (j & 3)];
+              const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(src));
+              const v4s hi4 =
+                  __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(src + 4 * VNP));
+              struct {
+                v4s a, b;
+              } both = {lo4, hi4};
+              acc = TR::mma(*reinterpret_cast<const u32x4*>(&Pw[(lane & 15) * VP + key]),
+                            __builtin_bit_cast(u32x4, both), acc);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wv[db][e] = wadd<BITS>(wv[db][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+          }
+          // one d block at a time: keeps the scheduler from hoisting every
+          // block's LDS reads (and their registers) to the top
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (nc != c) {  // end of the chunk: its denominators, then the fold
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
+            if (mx[e] == -__builtin_inff()) continue;  // no key of the row in this chunk
+            float Mn, fa, fb;
+            merge_factors(Mr[e], mx[e], Mn, fa, fb);
+            Dr[e] = wadd<BITS>(rescale<BITS>(Dr[e], fa), rescale<BITS>(den[e], fb));
+#pragma unroll
+            for (int b = 0; b < DBLK; ++b) Wr[b][e] = wadd<BITS>(rescale<BITS>(Wr[b][e], fa), rescale<BITS>(wv[b][e], fb));
+            Mr[e] = Mn;
+          }
+          reset();
+        }
+      }
+      if (!more) break;
+      c = nc;
+      phase = nphase;
+      t = nt;
+      buf ^= 1;
+    }
+  }
+
+  float den_f[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) den_f[e] = fmaxf(acc_f32<BITS>(Dr[e], a.fxp_inv), 1.0e-6f);
+  T* Op = static_cast<T*>(a.o);
+#pragma unroll
+  for (int b = 0; b < DBLK; ++b) {
+    const int d = b * 16 + (lane & 15);
+    if (d >= a.head_dim) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + 4 * kg + e);
+      if (!ri.valid) continue;
+      Op[ri.token * a.so_t + int64_t(ri.head) * a.so_h + d] =
+          Io<DT>::store(div_rn(acc_f32<BITS>(Wr[b][e], a.fxp_inv), den_f[e]));
+    }
+  }
+}
+
 // Fold the per-chunk partials of each (token, head) in ascending chunk order
 // (the kernel's single-pass fold, step for step) and divide.
 template <int DT, int BITS>
@@ -667,6 +976,14 @@ template <int DT, int BITS, int DMAX>
 int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st) {
   dim3 grid(unsigned(num_requests * a.num_kv_heads), unsigned(max_qtiles), unsigned(a.num_splits));
   if (a.num_splits <= 1) {
+    if constexpr (DT != FXPR_DTYPE_F32 && BITS <= 32 && DMAX <= 128) {
+      // prefill-shaped: 64-row tiles (same bits per row as attn_kernel)
+      if (int64_t(max_qtiles) * QROWS >= PQROWS) {
+        const int ptiles = int(cdiv(int64_t(max_qtiles) * QROWS, PQROWS));
+        attn_prefill_kernel<DT, BITS, DMAX><<<dim3(grid.x, unsigned(ptiles), 1), kPThreads, 0, st>>>(a);
+        return launch_status();
+      }
+    }
     attn_kernel<DT, BITS, DMAX, false><<<grid, kThreads, 0, st>>>(a);
     return launch_status();
   }
