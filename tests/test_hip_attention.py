@@ -320,3 +320,64 @@ def test_config4_decode_full_shape_properties():
         want = oracle(q[r:r + 1].cpu(), sub_kv, torch.tensor([0, 1], dtype=torch.int32),
                       sl[r:r + 1], sub_bt)
         assert close(ref[r:r + 1], want)
+
+
+# --------------------------------------------------------------------------
+# 128-row prefill workgroups (16-bit inputs, Q <= 32-bit accumulators,
+# head_dim <= 128, one split, max_query_len * group >= 113) against the
+# generic kernel's split path: the bits must not depend on which runs
+
+
+def _prefix_case(q_lens, ctxs, hq, hkv, d, ps, dtype, seed):
+    """Requests with a cached prefix of ctxs[i] keys and q_lens[i] new tokens,
+    pages shuffled over one pool."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    sls = [c + q for c, q in zip(ctxs, q_lens)]
+    maxb = max(-(-s // ps) for s in sls)
+    nb = len(sls) * maxb + 3
+    perm = torch.randperm(nb, generator=g)[: len(sls) * maxb].to(torch.int32)
+    bt = perm.reshape(len(sls), maxb)
+    T = sum(q_lens)
+    q = torch.randn(T, hq, d, generator=g).to(dtype)
+    kv = torch.randn(nb, 2, ps, hkv, d, generator=g).to(dtype)
+    qsl = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32)
+    sl = torch.tensor(sls, dtype=torch.int32)
+    return q.to(DEV), kv.to(DEV), qsl.to(DEV), sl.to(DEV), bt.to(DEV)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d,ps,group", [(128, 16, 4), (64, 1, 1), (96, 32, 2), (128, 16, 8)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_workgroups_match_split_path(dtype, d, ps, group, causal):
+    hkv = 2
+    args = _prefix_case([300, 45, 130], [700, 0, 1500], hkv * group, hkv, d, ps, dtype, seed=d + ps + group)
+    scale = 1 / math.sqrt(d)
+    one = attend(*args, 300, 1, causal=causal, scale=scale)
+    assert torch.equal(one, attend(*args, 300, 3, causal=causal, scale=scale))
+    assert torch.equal(one, attend(*args, 300, 0, causal=causal, scale=scale))
+
+
+@pytest.mark.parametrize("bits,frac", [(16, 8), (32, 16), (64, 32)])
+def test_prefill_workgroups_formats_windows_alibi_softcap(bits, frac):
+    dtype = torch.bfloat16
+    args = _prefix_case([260, 140], [600, 50], 8, 2, 128, 16, dtype, seed=bits)
+    slopes = torch.linspace(0.02, 0.5, 8, dtype=torch.float32, device=DEV)
+    kw = dict(scale=1 / math.sqrt(128), bits=bits, frac=frac, alibi=slopes, softcap=20.0, window=333)
+    one = attend(*args, 260, 1, **kw)
+    assert torch.equal(one, attend(*args, 260, 4, **kw))
+    tol = 5e-2 if bits == 16 else 1e-2
+    assert close(one, oracle(*args, scale=kw["scale"], bits=bits, frac=frac, alibi=slopes, softcap=20.0,
+                             window=333), tol)
+
+
+def test_prefill_rows_equal_their_decode_step():
+    # the last prompt token computed inside a 400-token prefill equals the
+    # same token computed as a one-token decode over the cached prefix
+    dtype = torch.bfloat16
+    q, kv, qsl, sl, bt = _prefix_case([400], [900], 32, 8, 128, 16, dtype, seed=3)
+    scale = 1 / math.sqrt(128)
+    full = attend(q, kv, qsl, sl, bt, 400, 1, scale=scale)
+    q1 = q[-1:].contiguous()
+    dec = attend(q1, kv, torch.tensor([0, 1], dtype=torch.int32, device=DEV), sl, bt, 1, 0, scale=scale)
+    assert torch.equal(full[-1:], dec)
+    assert close(full, oracle(q, kv, qsl, sl, bt, scale=scale))
