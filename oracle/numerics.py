@@ -176,8 +176,9 @@ def sat_sum_nonneg(q: np.ndarray, int_bits: int, axis: int = -1) -> np.ndarray:
 # ---------------------------------------------------------------------------
 # The build's own exp and log (no reference counterpart: the reference's
 # log-softmax file is absent, fxpr_vllm README.md:60). Cody-Waite style
-# reduction to a power of two plus a Taylor polynomial by Horner's rule, one
-# fp32 rounding per operation; the device restatement is csrc/fxp_device.h.
+# reduction to a power of two plus a Taylor polynomial by Horner's rule (exp:
+# fused multiply-adds; log: separate products and sums), one fp32 rounding per
+# operation; the device restatement is csrc/fxp_device.h.
 
 EXP2_C = [F32(c) for c in (
     1.0,
@@ -197,12 +198,42 @@ EXP_FLOOR = F32(-80.0)
 LOG_C = [F32(c) for c in (1.0, 1.0 / 3.0, 0.2, 1.0 / 7.0, 1.0 / 9.0)]
 
 
+def fma_f32(a, b, c) -> np.ndarray:
+    """fl32(a * b + c) with one rounding (round half to even): IEEE fused
+    multiply-add on fp32 operands.
+
+    The product of two fp32 values is exact in float64; the float64 sum s is
+    completed by its exact error e (TwoSum), so s + e = a*b + c exactly.
+    Rounding s to fp32 gives the correctly rounded result unless s lies
+    exactly half-way between two fp32 neighbours while e != 0: the tie then
+    goes to the neighbour on e's side. (|e| is at most half a float64 ulp of
+    s, far below half an fp32 ulp, so no other case can differ.)"""
+    a64 = np.asarray(a, dtype=np.float32).astype(np.float64)
+    b64 = np.asarray(b, dtype=np.float32).astype(np.float64)
+    c64 = np.asarray(c, dtype=np.float32).astype(np.float64)
+    p = a64 * b64
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = p + c64
+        bv = s - p
+        e = (p - (s - bv)) + (c64 - bv)
+        r = s.astype(np.float32)
+        r64 = r.astype(np.float64)
+        up = np.nextafter(r, np.float32(np.inf)).astype(np.float64)
+        dn = np.nextafter(r, np.float32(-np.inf)).astype(np.float64)
+        tie_up = (s == (r64 + up) * 0.5) & (e > 0)   # true sum just above an upper tie
+        tie_dn = (s == (r64 + dn) * 0.5) & (e < 0)   # true sum just below a lower tie
+    fin = np.isfinite(s) & np.isfinite(e)
+    out = np.where(fin & tie_up, up, np.where(fin & tie_dn, dn, r64))
+    return out.astype(np.float32)
+
+
 def exp2_poly(r: np.ndarray) -> np.ndarray:
-    """2^r for |r| <= 0.5: degree-7 Taylor polynomial, Horner."""
+    """2^r for |r| <= 0.5: degree-7 Taylor polynomial, Horner's rule with
+    fused multiply-adds (one rounding per step)."""
     r = np.asarray(r, dtype=np.float32)
     p = np.full_like(r, EXP2_C[7])
     for c in EXP2_C[6::-1]:
-        p = p * r + c
+        p = fma_f32(p, r, c)
     return p
 
 

@@ -263,3 +263,45 @@ def test_log_own_accuracy():
     err = np.abs(got - want)
     assert np.all(err <= 4e-7 * np.maximum(1.0, np.abs(want))), err.max()
     assert N.log_own(np.float32([1.0]))[0] == 0.0
+
+
+def _fma_exact(a, b, c):
+    """Correctly rounded fp32 of a*b + c by exact rational arithmetic."""
+    from fractions import Fraction
+    x = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    if x == 0:
+        return np.float32(0.0)
+    r = np.float32(float(x))  # float(x) rounds the exact value to float64 ...
+    # ... so pick among the fp32 neighbours of that guess by exact distance
+    cands = [np.nextafter(r, np.float32(-np.inf)), r, np.nextafter(r, np.float32(np.inf))]
+    best = None
+    for cnd in cands:
+        dist = abs(Fraction(float(cnd)) - x)
+        key = (dist, int(np.float32(cnd).view(np.uint32)) & 1)  # ties to the even significand
+        if best is None or key < best[0]:
+            best = (key, cnd)
+    return np.float32(best[1])
+
+
+def test_fma_f32_matches_exact_rounding():
+    rng = np.random.default_rng(0)
+    # random operands over a wide exponent range
+    a = (rng.standard_normal(3000) * 2.0 ** rng.integers(-20, 20, 3000)).astype(np.float32)
+    b = (rng.standard_normal(3000) * 2.0 ** rng.integers(-20, 20, 3000)).astype(np.float32)
+    c = (rng.standard_normal(3000) * 2.0 ** rng.integers(-40, 40, 3000)).astype(np.float32)
+    # integer operands: a*b + c lands exactly on fp32 ties often
+    ai = rng.integers(1, 1 << 13, 2000).astype(np.float32)
+    bi = rng.integers(1, 1 << 13, 2000).astype(np.float32)
+    ci = rng.integers(-(1 << 12), 1 << 12, 2000).astype(np.float32)
+    # double-rounding traps: a*b an exact fp32 tie (odd multiple of half an
+    # ulp at 2^25), c a tiny nudge of either sign that float64 alone loses
+    at = (2.0 * rng.integers(1 << 11, 1 << 12, 1000) + 1).astype(np.float32)   # odd, 12 bits
+    bt = (2.0 ** 13 * (2 * rng.integers(1 << 11, 1 << 12, 1000) + 1)).astype(np.float32)
+    ct = (rng.choice([-1.0, 1.0], 1000) * 2.0 ** rng.integers(-40, -20, 1000)).astype(np.float32)
+    A_ = np.concatenate([a, ai, at]); B_ = np.concatenate([b, bi, bt]); C_ = np.concatenate([c, ci, ct])
+    got = N.fma_f32(A_, B_, C_)
+    want = np.array([_fma_exact(x, y, z) for x, y, z in zip(A_, B_, C_)], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the trap cases really are ties that plain float64 evaluation gets wrong
+    naive = (at.astype(np.float64) * bt + ct).astype(np.float32)
+    assert (naive != N.fma_f32(at, bt, ct)).sum() > 100

@@ -151,16 +151,17 @@ __device__ __forceinline__ uint64_t sat_add_nonneg(uint64_t a, uint64_t b, uint6
 #define FXPR_SQRT2 1.41421356237309505f
 #define FXPR_EXP_FLOOR (-80.0f)
 
-// 2^r for |r| <= 0.5.
+// 2^r for |r| <= 0.5: Horner's rule with fused multiply-adds (v_fma_f32,
+// one rounding per step).
 __device__ __forceinline__ float exp2_poly(float r) {
   float p = FXPR_EXP2_C7;
-  p = __fadd_rn(__fmul_rn(p, r), FXPR_EXP2_C6);
-  p = __fadd_rn(__fmul_rn(p, r), FXPR_EXP2_C5);
-  p = __fadd_rn(__fmul_rn(p, r), FXPR_EXP2_C4);
-  p = __fadd_rn(__fmul_rn(p, r), FXPR_EXP2_C3);
-  p = __fadd_rn(__fmul_rn(p, r), FXPR_EXP2_C2);
-  p = __fadd_rn(__fmul_rn(p, r), FXPR_EXP2_C1);
-  p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+  p = __builtin_fmaf(p, r, FXPR_EXP2_C6);
+  p = __builtin_fmaf(p, r, FXPR_EXP2_C5);
+  p = __builtin_fmaf(p, r, FXPR_EXP2_C4);
+  p = __builtin_fmaf(p, r, FXPR_EXP2_C3);
+  p = __builtin_fmaf(p, r, FXPR_EXP2_C2);
+  p = __builtin_fmaf(p, r, FXPR_EXP2_C1);
+  p = __builtin_fmaf(p, r, 1.0f);
   return p;
 }
 
@@ -173,6 +174,17 @@ __device__ __forceinline__ float exp_scaled(float d, int f) {
   float t = __fmul_rn(d, FXPR_LOG2E);
   float k = __builtin_rintf(t);
   float r = __fsub_rn(t, k);
+  return __builtin_ldexpf(exp2_poly(r), static_cast<int>(k) + f);
+}
+
+// exp_scaled for a caller that rounds the result to an integer (f <= 63),
+// without a branch: d below the floor, or NaN, is raised to the floor, where
+// the result is below 2^-52 and rounds to 0 exactly as exp_scaled's 0 does.
+__device__ __forceinline__ float exp_scaled_to_round(float d, int f) {
+  d = fmaxf(d, FXPR_EXP_FLOOR);  // maxNum: NaN -> the floor
+  const float t = __fmul_rn(d, FXPR_LOG2E);
+  const float k = __builtin_rintf(t);
+  const float r = __fsub_rn(t, k);
   return __builtin_ldexpf(exp2_poly(r), static_cast<int>(k) + f);
 }
 

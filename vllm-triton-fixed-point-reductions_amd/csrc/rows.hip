@@ -10,6 +10,8 @@
 // in registers between the reduction pass and the output pass so x is read
 // from HBM once.
 
+#include <type_traits>
+
 #include "fxp_device.h"
 #include "fxpr_internal.h"
 
@@ -325,12 +327,21 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
   }
   m = block_max(m, fred);
 
-  uint64_t acc = 0;
+  // Terms are in [0, qmax]; for qmax < 2^31 a 32-bit min(a + b, qmax) is
+  // the same saturating sum as the 64-bit one.
+  using SumT = typename std::conditional<BITS == 64, uint64_t, uint32_t>::type;
+  SumT acc = 0;
   auto accum = [&](const XV& xv) {
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
       const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
-      acc = sat_add_nonneg(acc, quant_nonneg<BITS>(exp_scaled(d, frac)), qmax);
+      const uint64_t q = quant_nonneg<BITS>(exp_scaled_to_round(d, frac));
+      if constexpr (BITS == 64) {
+        acc = sat_add_nonneg(acc, q, qmax);
+      } else {
+        const uint32_t s32 = acc + static_cast<uint32_t>(q);
+        acc = s32 < static_cast<uint32_t>(qmax) ? s32 : static_cast<uint32_t>(qmax);
+      }
     }
   };
 #pragma unroll
@@ -339,7 +350,7 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
     if (c < nchunks) accum(keep[i]);
   }
   for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum(xr[c]);
-  const uint64_t total = block_sat_sum(acc, qmax, ired);
+  const uint64_t total = block_sat_sum(static_cast<uint64_t>(acc), qmax, ired);
 
   const float lnS = total == 0 ? -__builtin_inff()
                                : log_own(fixed_to_f32(static_cast<int64_t>(total), inv_scale));
