@@ -30,12 +30,12 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 }
 
 // fp32 -> bf16, round half to even; NaN becomes the canonical 0x7FC0 (the
-// same rule torch uses on the CPU).
+// same rule torch uses on the CPU). The conversion is gfx950's
+// v_cvt_pk_bf16_f32 (round half to even, denormals kept); only the NaN
+// payload rule is applied on top.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  return f != f ? static_cast<uint16_t>(0x7fc0u) : h;
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
