@@ -381,3 +381,20 @@ def test_prefill_rows_equal_their_decode_step():
     dec = attend(q1, kv, torch.tensor([0, 1], dtype=torch.int32, device=DEV), sl, bt, 1, 0, scale=scale)
     assert torch.equal(full[-1:], dec)
     assert close(full, oracle(q, kv, qsl, sl, bt, scale=scale))
+
+
+def test_mixed_batch_routes_each_request_and_keeps_bits():
+    # decode steps, a short prompt (below the prefill-workgroup threshold)
+    # and a long prompt in one launch: each request's output equals the
+    # request run alone
+    dtype = torch.bfloat16
+    q_lens, ctxs = [1, 300, 1, 5, 1], [2000, 700, 517, 40, 3000]
+    q, kv, qsl, sl, bt = _prefix_case(q_lens, ctxs, 32, 8, 128, 16, dtype, seed=21)
+    scale = 1 / math.sqrt(128)
+    both = attend(q, kv, qsl, sl, bt, max(q_lens), 0, scale=scale)
+    starts = [0] + list(np.cumsum(q_lens))
+    for i, ql in enumerate(q_lens):
+        qi = q[starts[i]:starts[i] + ql].contiguous()
+        alone = attend(qi, kv, torch.tensor([0, ql], dtype=torch.int32, device=DEV), sl[i:i + 1].contiguous(),
+                       bt[i:i + 1].contiguous(), ql, 0, scale=scale)
+        assert torch.equal(both[starts[i]:starts[i] + ql], alone), i

@@ -68,6 +68,7 @@ struct AttnArgs {
   int max_blocks;       // block-table row length
   int chunks_per_split;  // > 0: fixed chunks per split (work-balanced); 0: even division
   int chunk_slots;       // chunks per row in the split workspace
+  int pq_rows;           // > 0: requests with at least this many rows go to attn_prefill_kernel
   int num_requests;
   int64_t num_blocks;   // physical blocks in the cache
   int64_t num_tokens;   // rows of q / o
@@ -228,6 +229,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   const int rows_total = q_len * a.group;
   const int row0 = qt * QROWS;
   if (row0 >= rows_total) return;  // uniform
+  if (a.pq_rows > 0 && rows_total >= a.pq_rows) return;  // attn_prefill_kernel's request
 
   // Key range of the workgroup (union over its rows), in absolute tiles, and
   // the absolute key chunks (CT tiles) it touches. A chunk's statistics are
@@ -623,6 +625,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 // exact zeros, so the workgroup's wider key range changes nothing) and the
 // same fold.
 constexpr int PQ_WAVES = 8;
+// Requests with at least this many rows (query tokens x GQA group) use the
+// prefill workgroups: from three 16-row tiles on, reading each key tile
+// three times (K twice, V once) per 128 rows costs less than twice per 16.
+constexpr int kPrefillRows = 48;
 constexpr int PQROWS = 16 * PQ_WAVES;
 constexpr int kPThreads = 64 * PQ_WAVES;
 
@@ -658,7 +664,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_kernel(AttnArgs a) 
   const int ctx = seq_len - q_len;
   const int rows_total = q_len * a.group;
   const int row0 = blockIdx.y * PQROWS;
-  if (row0 >= rows_total) return;  // uniform
+  if (row0 >= rows_total || rows_total < a.pq_rows) return;  // uniform; short requests: attn_kernel
   const int wrow0 = row0 + 16 * wave;
 
   const int i_min = row0 / a.group;
@@ -977,10 +983,16 @@ int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num
   dim3 grid(unsigned(num_requests * a.num_kv_heads), unsigned(max_qtiles), unsigned(a.num_splits));
   if (a.num_splits <= 1) {
     if constexpr (DT != FXPR_DTYPE_F32 && BITS <= 32 && DMAX <= 128) {
-      // prefill-shaped: 64-row tiles (same bits per row as attn_kernel)
-      if (int64_t(max_qtiles) * QROWS >= PQROWS) {
+      // Requests of at least kPrefillRows rows run in 128-row workgroups,
+      // the others (decode steps, short prompts) in attn_kernel's 16-row
+      // ones; both kernels see the whole batch and each skips the other's
+      // requests. Same bits per row either way.
+      if (int64_t(max_qtiles) * QROWS >= kPrefillRows) {
+        AttnArgs b = a;
+        b.pq_rows = kPrefillRows;
         const int ptiles = int(cdiv(int64_t(max_qtiles) * QROWS, PQROWS));
-        attn_prefill_kernel<DT, BITS, DMAX><<<dim3(grid.x, unsigned(ptiles), 1), kPThreads, 0, st>>>(a);
+        attn_prefill_kernel<DT, BITS, DMAX><<<dim3(grid.x, unsigned(ptiles), 1), kPThreads, 0, st>>>(b);
+        attn_kernel<DT, BITS, DMAX, false><<<grid, kThreads, 0, st>>>(b);
         return launch_status();
       }
     }
