@@ -615,6 +615,454 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   }
 }
 
+// Decode-shaped launches through LDS DMA (16-bit inputs, head_dim 64 or 128,
+// power-of-two pages of at least 16 keys): attn_kernel's 16-row workgroups,
+// chunks and bits, with the K and V tiles brought into an NS-stage LDS ring
+// by global_load_lds instead of through registers. Each wave moves 16
+// consecutive key rows of a tile, all in one page, so its page entry is one
+// scalar load, issued a step before the DMAs that use it (no vector-memory
+// traffic besides the DMAs, whose count the explicit waits rely on). LDS rows hold 16-byte chunk c of key row r at
+// slot c ^ dswz(r): the K fragment reads (16 consecutive rows, one chunk
+// each) and the transposing V reads (4 consecutive rows, 32 bytes each) hit
+// distinct banks. Every LDS access in the pipelined loop is inline asm: the
+// compiler would otherwise wait for all DMAs in flight before it.
+template <int DMAX> struct DmaGeom {
+  static constexpr int ROWB = DMAX * 2;          // bytes per key row
+  static constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
+  static constexpr int KPI = 1024 / ROWB;        // key rows per wave instruction
+  static constexpr int TILEB = TILE * ROWB;      // bytes per tile
+  static constexpr int NDMA = TILEB / (kThreads * 16);  // DMA instructions per thread per tile
+  static constexpr int NS = 3;                   // LDS stages
+  static __device__ __forceinline__ int swz(int r) {
+    if constexpr (CPR >= 16) {
+      return ((r & 3) << 2) | ((r >> 2) & 3);
+    } else {
+      const int q = (r >> 1) & 7;  // 128-byte rows: pairs share a 256-byte bank window
+      return ((q << 1) | (q >> 2)) & 7;
+    }
+  }
+};
+
+typedef __attribute__((address_space(3))) void* AttnLdsPtr;
+typedef const __attribute__((address_space(4))) int32_t* ConstI32Ptr;
+
+__device__ __forceinline__ void lds_read_b128(unsigned addr, u32x4& x) {
+  asm volatile("ds_read_b128 %0, %1" : "=v"(x) : "v"(addr) : "memory");
+}
+__device__ __forceinline__ void lds_read_b64_tr16(unsigned addr, uint64_t& x) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(x) : "v"(addr) : "memory");
+}
+__device__ __forceinline__ void lds_read_b32(unsigned addr, uint32_t& x) {
+  asm volatile("ds_read_b32 %0, %1" : "=v"(x) : "v"(addr) : "memory");
+}
+__device__ __forceinline__ void lds_write_b16(unsigned addr, uint32_t x) {
+  asm volatile("ds_write_b16 %0, %1" ::"v"(addr), "v"(x) : "memory");
+}
+__device__ __forceinline__ void lds_write_b32(unsigned addr, uint32_t x) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(x) : "memory");
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// The wait, tied to the registers the reads filled: their uses cannot move
+// above it (the asm reads' outputs are otherwise "ready" at issue).
+template <class A> __device__ __forceinline__ void lds_wait_for(A& a) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a) : : "memory");
+}
+template <class A, class B> __device__ __forceinline__ void lds_wait_for(A& a, B& b) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b) : : "memory");
+}
+template <class A, class B, class C> __device__ __forceinline__ void lds_wait_for(A& a, B& b, C& c) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c) : : "memory");
+}
+template <class A, class B, class C, class D>
+__device__ __forceinline__ void lds_wait_for(A& a, B& b, C& c, D& d) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : : "memory");
+}
+
+template <int DT, int BITS, int DMAX, bool SPLIT>
+__global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
+  static_assert(DT != FXPR_DTYPE_F32, "16-bit inputs only");
+  using TR = Traits<DT>;
+  using T = typename TR::T;
+  using AccT = typename AccOf<BITS>::T;
+  using G = DmaGeom<DMAX>;
+  constexpr int KI = TR::KI, QUNIT = TR::QUNIT;
+  constexpr int QSTEPS = DMAX / KI;
+  constexpr int DBLK = DMAX / 16;
+  constexpr int DB_PER_WAVE = (DBLK + 3) / 4;
+  constexpr int VP = TILE + 8;             // Ps row pitch (elements)
+  constexpr int NS = G::NS;
+  // LDS: NS tile stages | weights Ps[CT][16][VP] | red_f[4][16] | red_i[4][16]
+  constexpr int PS_OFF = NS * G::TILEB;
+  constexpr int RF_OFF = PS_OFF + CT * QROWS * VP * 2;
+  constexpr int RI_OFF = RF_OFF + 4 * QROWS * 4;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(smem_raw));
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, kg = lane >> 4;
+  const int r = blockIdx.x / a.num_kv_heads, g = blockIdx.x % a.num_kv_heads;
+  const int qt = blockIdx.y, split = blockIdx.z;
+  const int q_start = a.qsl[r];
+  const int q_len = a.qsl[r + 1] - q_start;
+  const int seq_len = a.seq_lens[r];
+  const int ctx = seq_len - q_len;
+  const int rows_total = q_len * a.group;
+  const int row0 = qt * QROWS;
+  if (row0 >= rows_total) return;  // uniform
+  if (a.pq_rows > 0 && rows_total >= a.pq_rows) return;  // attn_prefill_kernel's request
+
+  const int i_min = row0 / a.group;
+  const int i_max = min(rows_total - 1, row0 + QROWS - 1) / a.group;
+  const int hi = a.causal ? min(seq_len, ctx + i_max + 1) : seq_len;
+  const int lo = a.window > 0 ? max(0, ctx + i_min - a.window + 1) : 0;
+  const int t_lo = lo / TILE;
+  const int t_hi = hi > lo ? (hi + TILE - 1) / TILE : t_lo;
+  const int c_lo = t_lo / CT;
+  int c_hi = t_hi > t_lo ? (t_hi + CT - 1) / CT : c_lo;
+  if constexpr (SPLIT) c_hi = min(c_hi, a.chunk_slots);
+  const int nch = max(0, c_hi - c_lo);
+  const int per = a.chunks_per_split > 0 ? a.chunks_per_split : (nch + a.num_splits - 1) / a.num_splits;
+  const int my_lo = SPLIT ? c_lo + min(nch, split * per) : c_lo;
+  const int my_hi = SPLIT ? min(c_lo + nch, my_lo + per) : c_lo + nch;
+
+  const T* Qp = static_cast<const T*>(a.q);
+  const ConstI32Ptr bt_row = (ConstI32Ptr)(a.bt + int64_t(r) * a.sbt);
+  const int last_block = int(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
+
+  // Q fragments (MFMA A operand): lane holds row lane%16, its k slots.
+  u32x4 qf[QSTEPS];
+  {
+    const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + (lane & 15));
+    const T* qbase = Qp + qrow.token * a.sq_t + int64_t(qrow.head) * a.sq_h;
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) {
+      const int d = 32 * j + 8 * kg;
+      qf[j] = qrow.valid ? *reinterpret_cast<const u32x4*>(qbase + d) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // Score-layout rows 4*kg + e as valid key ranges (empty outside the request).
+  int ks[4], ke[4], qp[4];
+  float slope[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + 4 * kg + e);
+    ks[e] = ri.valid ? ri.kstart : 0x7fffffff;
+    ke[e] = ri.valid ? ri.kend : 0;
+    qp[e] = ri.qpos;
+    slope[e] = a.alibi ? a.alibi[ri.head] : 0.0f;
+  }
+  if (SPLIT && split == 0 && tid < QROWS) {
+    const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
+    if (ri.valid) {
+      int* cr = a.crange + 2 * (ri.token * a.num_heads + ri.head);
+      cr[0] = c_lo;
+      cr[1] = c_lo + nch;
+    }
+  }
+
+  // Per-lane LDS offsets within a stage.
+  // K fragment j of the lane's key (row wave*16 + lane%16), chunk 4j + kg.
+  unsigned koff[QSTEPS];
+  {
+    const int rr = wave * 16 + (lane & 15);
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) koff[j] = rr * G::ROWB + ((((4 * j + kg) ^ G::swz(rr))) << 4);
+  }
+  // V B-operand reads (ds_read_b64_tr_b16): d block db = wave + 4b, keys
+  // k0 + 8kg + (j>>2) (+4 for the upper half), columns db*16 + 4*(j&3).
+  constexpr int NK0 = QUNIT / KI;  // MFMA k steps per quantised chain (2)
+  unsigned voff[DB_PER_WAVE][NK0][2];
+#pragma unroll
+  for (int b = 0; b < DB_PER_WAVE; ++b)
+#pragma unroll
+    for (int s = 0; s < NK0; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int db = min(wave + 4 * b, DBLK - 1);
+        const int j = lane & 15;
+        const int rr = s * KI + 8 * kg + (j >> 2) + 4 * h;
+        const int c = 2 * db + ((j & 3) >> 1);
+        voff[b][s][h] = rr * G::ROWB + ((c ^ G::swz(rr)) << 4) + (j & 1) * 8;
+      }
+
+  // DMA of tile t (K or V) into stage buf: the wave moves key rows
+  // 16 wave .. 16 wave + 15 (one page), instruction q rows 16 wave + q*KPI
+  // .. +KPI-1, lane l row +l/CPR, slot l%CPR, i.e. chunk slot ^ swz(row).
+  const T* Kc = static_cast<const T*>(a.k);
+  const T* Vc = static_cast<const T*>(a.v);
+  auto page_entry = [&](int t) -> int {  // the wave's page of tile t (keys clamped)
+    const int key0 = min(t * TILE + 16 * wave, seq_len - 1);
+    const int lb = __builtin_amdgcn_readfirstlane(key0 >> a.ps_shift);
+    return bt_row[min(lb, a.max_blocks - 1)];
+  };
+  auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
+    const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
+#pragma unroll
+    for (int q = 0; q < G::NDMA; ++q) {
+      const int row0q = 16 * wave + q * G::KPI;
+      const int rr = row0q + lane / G::CPR;
+      const int key = min(t * TILE + rr, seq_len - 1);
+      const int c = (lane % G::CPR) ^ G::swz(rr);
+      const int64_t sb = isv ? a.sv_b : a.sk_b, ss = isv ? a.sv_s : a.sk_s, sh = isv ? a.sv_h : a.sk_h;
+      const uint64_t off = uint64_t(p) * uint32_t(sb) + uint64_t(uint32_t(key & (a.page_size - 1))) * uint32_t(ss) +
+                           uint64_t(uint32_t(g)) * uint32_t(sh) + uint32_t(c * 8);
+      const T* src = (isv ? Vc : Kc) + off;
+      const unsigned dst = lds0 + buf * G::TILEB + row0q * G::ROWB;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
+    }
+  };
+
+  float Mr[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  AccT Dr[4] = {0, 0, 0, 0};
+  AccT Wr[DB_PER_WAVE][4];
+#pragma unroll
+  for (int b = 0; b < DB_PER_WAVE; ++b)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Wr[b][e] = 0;
+
+  if (my_lo < my_hi) {
+    // Steps: per chunk its live K tiles, then the same V tiles. Step s uses
+    // stage s % NS; its DMAs were issued NS - 1 steps earlier (past the last
+    // step the last tile is re-issued into the free stage, so every step
+    // issues the same number of DMAs and the wait count stays exact).
+    auto live_lo = [&](int cc) { return max(cc * CT, t_lo); };
+    auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
+    // the step after (cc, isv, t)
+    auto advance = [&](int& cc, bool& isv, int& t) {
+      if (++t < live_hi(cc)) return;
+      if (!isv) {
+        isv = true;
+        t = live_lo(cc);
+      } else if (cc + 1 < my_hi) {
+        ++cc;
+        isv = false;
+        t = live_lo(cc);
+      } else {
+        t = live_hi(cc) - 1;  // past the end: re-issue the last tile
+      }
+    };
+    // The Q and row-setup loads land first (an s_waitcnt the compiler sees,
+    // so it does not later wait for them behind the DMAs).
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    int dc_ = my_lo, dt = live_lo(my_lo);  // DMA cursor
+    bool dv = false;
+    int dent = page_entry(dt);  // page entry at the cursor
+#pragma unroll
+    for (int i = 0; i + 1 < NS; ++i) {
+      dma_tile(dv, dt, dent, i);
+      advance(dc_, dv, dt);
+      dent = page_entry(dt);
+    }
+
+    float sc[CT][4];
+    float mx[4];
+    AccT den[4];
+    AccT wv[DB_PER_WAVE][4];
+    int step = 0;
+    for (int c = my_lo; c < my_hi; ++c) {
+      const int ta = live_lo(c), te = live_hi(c), nt = te - ta;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        mx[e] = -__builtin_inff();
+        den[e] = 0;
+      }
+#pragma unroll
+      for (int b = 0; b < DB_PER_WAVE; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[b][e] = 0;
+      auto step_begin = [&]() -> unsigned {
+        // own DMAs of this step landed (only later steps' in flight), own
+        // LDS writes done; the barrier makes both everyone's
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(G::NDMA * (NS - 2)) : "memory");
+        __builtin_amdgcn_s_barrier();
+        dma_tile(dv, dt, dent, (step + NS - 1) % NS);
+        advance(dc_, dv, dt);
+        dent = page_entry(dt);  // for the next step's DMAs
+        const unsigned base = lds0 + (step % NS) * G::TILEB;
+        ++step;
+        return base;
+      };
+      // K half: scores of the live tiles into registers, then the row maxima.
+#pragma unroll
+      for (int u = 0; u < CT; ++u) {
+        if (u < nt) {
+          const unsigned base = step_begin();
+          u32x4 kf[QSTEPS];
+#pragma unroll
+          for (int j = 0; j < QSTEPS; ++j) lds_read_b128(base + koff[j], kf[j]);
+          if constexpr (QSTEPS == 4) lds_wait_for(kf[0], kf[1], kf[2], kf[3]);
+          else lds_wait_for(kf[0], kf[1]);
+          const int t = ta + u;
+          const int key = t * TILE + wave * 16 + (lane & 15);
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < QSTEPS; ++j) acc = TR::mma(qf[j], kf[j], acc);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float x = __fmul_rn(acc[e], a.scale_log2);
+            if (a.softcap_log2 > 0.0f) x = a.softcap_log2 * tanh_approx(x / a.softcap_log2);
+            if (a.alibi) x = x + slope[e] * static_cast<float>(key - qp[e]);
+            sc[u][e] = (key >= ks[e] && key < ke[e]) ? x : -__builtin_inff();
+            mx[e] = fmaxf(mx[e], sc[u][e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[u][e] = -__builtin_inff();
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o, 64));
+        if ((lane & 15) == 0) lds_write_b32(lds0 + RF_OFF + (wave * QROWS + 4 * kg + e) * 4, __float_as_uint(mx[e]));
+      }
+      lds_wait();
+      __builtin_amdgcn_s_barrier();
+      float mc[4], m[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t v[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) lds_read_b32(lds0 + RF_OFF + (w * QROWS + 4 * kg + e) * 4, v[w]);
+        lds_wait_for(v[0], v[1], v[2], v[3]);
+        mc[e] = fmaxf(fmaxf(__uint_as_float(v[0]), __uint_as_float(v[1])),
+                      fmaxf(__uint_as_float(v[2]), __uint_as_float(v[3])));
+        m[e] = mc[e] != -__builtin_inff() ? mc[e] : 0.0f;  // no key: pin to 0
+      }
+      // Weights of every live tile of the chunk into Ps (visible to all after
+      // the next step's barrier), denominators on the way.
+      const int kin = wave * 16 + (lane & 15);
+#pragma unroll
+      for (int u = 0; u < CT; ++u) {
+        if (u < nt) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float w = __builtin_amdgcn_exp2f(sc[u][e] - m[e]);
+            den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
+            lds_write_b16(lds0 + PS_OFF + ((u * QROWS + 4 * kg + e) * VP + kin) * 2, Io<DT>::store(w));
+          }
+        }
+      }
+      // V half: weighted V of the live tiles.
+#pragma unroll
+      for (int u = 0; u < CT; ++u) {
+        if (u < nt) {
+          const unsigned base = step_begin();
+#pragma unroll
+          for (int b = 0; b < DB_PER_WAVE; ++b) {
+            if (wave + 4 * b < DBLK) {
+              f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int s = 0; s < NK0; ++s) {
+                u32x4 pa;
+                uint64_t lo2, hi2;
+                lds_read_b128(lds0 + PS_OFF + ((u * QROWS + (lane & 15)) * VP + s * KI + 8 * kg) * 2, pa);
+                lds_read_b64_tr16(base + voff[b][s][0], lo2);
+                lds_read_b64_tr16(base + voff[b][s][1], hi2);
+                lds_wait_for(pa, lo2, hi2);
+                const u32x4 vb = {uint32_t(lo2), uint32_t(lo2 >> 32), uint32_t(hi2), uint32_t(hi2 >> 32)};
+                acc = TR::mma(pa, vb, acc);
+              }
+#pragma unroll
+              for (int e = 0; e < 4; ++e) wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+            }
+          }
+        }
+      }
+      // The chunk's denominators: 16 key lanes, then the 4 waves.
+      AccT dc[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
+      }
+      if ((lane & 15) == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const unsigned ad = lds0 + RI_OFF + (wave * QROWS + 4 * kg + e) * 8;
+          const uint64_t v = static_cast<uint64_t>(static_cast<int64_t>(den[e]));
+          lds_write_b32(ad, uint32_t(v));
+          lds_write_b32(ad + 4, uint32_t(v >> 32));
+        }
+      }
+      lds_wait();
+      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        AccT sum = 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          uint32_t lo32, hi32;
+          const unsigned ad = lds0 + RI_OFF + (w * QROWS + 4 * kg + e) * 8;
+          lds_read_b32(ad, lo32);
+          lds_read_b32(ad + 4, hi32);
+          lds_wait_for(lo32, hi32);
+          const int64_t v = static_cast<int64_t>((uint64_t(hi32) << 32) | lo32);
+          sum = wadd<BITS>(sum, v);
+        }
+        dc[e] = sum;
+      }
+
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + 4 * kg + e);
+          if (!ri.valid) continue;
+          const int64_t slot = (ri.token * a.num_heads + ri.head) * a.chunk_slots + c;
+          if ((lane & 15) == 0 && wave == 0) {
+            a.pmax[slot] = mc[e];
+            static_cast<AccT*>(a.den_ws)[slot] = dc[e];
+          }
+#pragma unroll
+          for (int b = 0; b < DB_PER_WAVE; ++b) {
+            const int d = (wave + 4 * b) * 16 + (lane & 15);
+            if (wave + 4 * b < DBLK) static_cast<AccT*>(a.wv_ws)[slot * a.head_dim + d] = wv[b][e];
+          }
+        }
+        // the stores count in vmcnt: let them (and the DMAs ahead) land so
+        // the next chunk's explicit waits count only its own DMAs
+        if (c + 1 < my_hi) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (mc[e] == -__builtin_inff()) continue;
+          float Mn, fa, fb;
+          merge_factors(Mr[e], mc[e], Mn, fa, fb);
+          Dr[e] = wadd<BITS>(rescale<BITS>(Dr[e], fa), rescale<BITS>(dc[e], fb));
+#pragma unroll
+          for (int b = 0; b < DB_PER_WAVE; ++b)
+            Wr[b][e] = wadd<BITS>(rescale<BITS>(Wr[b][e], fa), rescale<BITS>(wv[b][e], fb));
+          Mr[e] = Mn;
+        }
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // DMAs into unused stages
+  }
+
+  if constexpr (!SPLIT) {
+    float den_f[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) den_f[e] = fmaxf(acc_f32<BITS>(Dr[e], a.fxp_inv), 1.0e-6f);
+    T* Op = static_cast<T*>(a.o);
+#pragma unroll
+    for (int b = 0; b < DB_PER_WAVE; ++b) {
+      const int d = (wave + 4 * b) * 16 + (lane & 15);
+      if (wave + 4 * b >= DBLK) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + 4 * kg + e);
+        if (!ri.valid) continue;
+        Op[ri.token * a.so_t + int64_t(ri.head) * a.so_h + d] =
+            Io<DT>::store(div_rn(acc_f32<BITS>(Wr[b][e], a.fxp_inv), den_f[e]));
+      }
+    }
+  }
+}
+
+template <int DMAX> constexpr size_t dma_lds_bytes() {
+  return size_t(DmaGeom<DMAX>::NS) * DmaGeom<DMAX>::TILEB + size_t(CT) * QROWS * (TILE + 8) * 2 + 4 * QROWS * 4 +
+         4 * QROWS * 8;
+}
+
 // Prefill-shaped launches (16-bit inputs, one split): 64 query rows per
 // workgroup, each wave owning 16 of them, so a key tile staged in LDS serves
 // four times the rows of attn_kernel's 16-row tile. A chunk's scores are not
@@ -978,9 +1426,37 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t n
       Io<DT>::store(div_rn(acc_f32<BITS>(W, a.fxp_inv), den_f));
 }
 
+// attn_dma_kernel serves a launch when each wave's 16 key rows of a tile lie
+// in one page and the rows are exactly DMAX wide.
+template <int DT, int DMAX> bool dma_ok(const AttnArgs& a) {
+  if constexpr (DT == FXPR_DTYPE_F32 || (DMAX != 64 && DMAX != 128)) {
+    return false;
+  } else {
+    return a.head_dim == DMAX && a.ps_shift >= 4;  // pages of 16, 32, ... keys
+  }
+}
+
+template <int DT, int BITS, int DMAX, bool SPLIT>
+int launch_dma(const AttnArgs& a, dim3 grid, hipStream_t st) {
+  if constexpr (DT != FXPR_DTYPE_F32 && (DMAX == 64 || DMAX == 128)) {
+    auto kern = attn_dma_kernel<DT, BITS, DMAX, SPLIT>;
+    constexpr size_t lds = dma_lds_bytes<DMAX>();
+    static bool attr_done = false;  // benign race: the attribute is idempotent
+    if (!attr_done) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+      if (e != hipSuccess) return int(e);
+      attr_done = true;
+    }
+    kern<<<grid, kThreads, lds, st>>>(a);
+  }
+  return 0;
+}
+
 template <int DT, int BITS, int DMAX>
 int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st) {
   dim3 grid(unsigned(num_requests * a.num_kv_heads), unsigned(max_qtiles), unsigned(a.num_splits));
+  const bool dma = dma_ok<DT, DMAX>(a);
   if (a.num_splits <= 1) {
     if constexpr (DT != FXPR_DTYPE_F32 && BITS <= 32 && DMAX <= 128) {
       // Requests of at least kPrefillRows rows run in 128-row workgroups,
@@ -992,14 +1468,29 @@ int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num
         b.pq_rows = kPrefillRows;
         const int ptiles = int(cdiv(int64_t(max_qtiles) * QROWS, PQROWS));
         attn_prefill_kernel<DT, BITS, DMAX><<<dim3(grid.x, unsigned(ptiles), 1), kPThreads, 0, st>>>(b);
-        attn_kernel<DT, BITS, DMAX, false><<<grid, kThreads, 0, st>>>(b);
+        if (dma) {
+          const int e = launch_dma<DT, BITS, DMAX, false>(b, grid, st);
+          if (e) return e;
+        } else {
+          attn_kernel<DT, BITS, DMAX, false><<<grid, kThreads, 0, st>>>(b);
+        }
         return launch_status();
       }
     }
-    attn_kernel<DT, BITS, DMAX, false><<<grid, kThreads, 0, st>>>(a);
+    if (dma) {
+      const int e = launch_dma<DT, BITS, DMAX, false>(a, grid, st);
+      if (e) return e;
+    } else {
+      attn_kernel<DT, BITS, DMAX, false><<<grid, kThreads, 0, st>>>(a);
+    }
     return launch_status();
   }
-  attn_kernel<DT, BITS, DMAX, true><<<grid, kThreads, 0, st>>>(a);
+  if (dma) {
+    const int e = launch_dma<DT, BITS, DMAX, true>(a, grid, st);
+    if (e) return e;
+  } else {
+    attn_kernel<DT, BITS, DMAX, true><<<grid, kThreads, 0, st>>>(a);
+  }
   const int64_t total = num_tokens * a.num_heads * a.head_dim;
   attn_combine_kernel<DT, BITS><<<dim3(unsigned(cdiv(total, 256))), 256, 0, st>>>(a, num_tokens);
   return launch_status();
