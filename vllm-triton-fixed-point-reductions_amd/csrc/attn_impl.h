@@ -632,7 +632,7 @@ template <int DMAX> struct DmaGeom {
   static constexpr int KPI = 1024 / ROWB;        // key rows per wave instruction
   static constexpr int TILEB = TILE * ROWB;      // bytes per tile
   static constexpr int NDMA = TILEB / (kThreads * 16);  // DMA instructions per thread per tile
-  static constexpr int NS = 3;                   // LDS stages
+  static constexpr int NS = 4;                   // LDS stages
   static __device__ __forceinline__ int swz(int r) {
     if constexpr (CPR >= 16) {
       return ((r & 3) << 2) | ((r >> 2) & 3);
@@ -691,9 +691,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   constexpr int DB_PER_WAVE = (DBLK + 3) / 4;
   constexpr int VP = TILE + 8;             // Ps row pitch (elements)
   constexpr int NS = G::NS;
-  // LDS: NS tile stages | weights Ps[CT][16][VP] | red_f[4][16] | red_i[4][16]
+  // LDS: NS tile stages | weights Ps[2][16][VP] | red_f[4][16] | red_i[4][16]
   constexpr int PS_OFF = NS * G::TILEB;
-  constexpr int RF_OFF = PS_OFF + CT * QROWS * VP * 2;
+  constexpr int RF_OFF = PS_OFF + 2 * QROWS * VP * 2;
   constexpr int RI_OFF = RF_OFF + 4 * QROWS * 4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(smem_raw));
@@ -928,20 +928,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
                       fmaxf(__uint_as_float(v[2]), __uint_as_float(v[3])));
         m[e] = mc[e] != -__builtin_inff() ? mc[e] : 0.0f;  // no key: pin to 0
       }
-      // Weights of every live tile of the chunk into Ps (visible to all after
-      // the next step's barrier), denominators on the way.
+      // Weights of live tile u into Ps[u & 1], denominators on the way. Tile
+      // 0's go in now, tile u + 1's during V step u; the next step's barrier
+      // publishes them (Ps[u & 1] was last read two V steps earlier).
       const int kin = wave * 16 + (lane & 15);
+      auto write_p = [&](int u) __attribute__((always_inline)) {
 #pragma unroll
-      for (int u = 0; u < CT; ++u) {
-        if (u < nt) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float w = __builtin_amdgcn_exp2f(sc[u][e] - m[e]);
-            den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
-            lds_write_b16(lds0 + PS_OFF + ((u * QROWS + 4 * kg + e) * VP + kin) * 2, Io<DT>::store(w));
-          }
+        for (int e = 0; e < 4; ++e) {
+          const float w = __builtin_amdgcn_exp2f(sc[u][e] - m[e]);
+          den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w, a.fxp_scale)));
+          lds_write_b16(lds0 + PS_OFF + (((u & 1) * QROWS + 4 * kg + e) * VP + kin) * 2, Io<DT>::store(w));
         }
-      }
+      };
+      write_p(0);
       // V half: weighted V of the live tiles.
 #pragma unroll
       for (int u = 0; u < CT; ++u) {
@@ -955,7 +954,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
               for (int s = 0; s < NK0; ++s) {
                 u32x4 pa;
                 uint64_t lo2, hi2;
-                lds_read_b128(lds0 + PS_OFF + ((u * QROWS + (lane & 15)) * VP + s * KI + 8 * kg) * 2, pa);
+                lds_read_b128(lds0 + PS_OFF + (((u & 1) * QROWS + (lane & 15)) * VP + s * KI + 8 * kg) * 2, pa);
                 lds_read_b64_tr16(base + voff[b][s][0], lo2);
                 lds_read_b64_tr16(base + voff[b][s][1], hi2);
                 lds_wait_for(pa, lo2, hi2);
@@ -966,6 +965,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
               for (int e = 0; e < 4; ++e) wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
             }
           }
+          if (u + 1 < nt) write_p(u + 1);
         }
       }
       // The chunk's denominators: 16 key lanes, then the 4 waves.
@@ -1059,7 +1059,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
 }
 
 template <int DMAX> constexpr size_t dma_lds_bytes() {
-  return size_t(DmaGeom<DMAX>::NS) * DmaGeom<DMAX>::TILEB + size_t(CT) * QROWS * (TILE + 8) * 2 + 4 * QROWS * 4 +
+  return size_t(DmaGeom<DMAX>::NS) * DmaGeom<DMAX>::TILEB + size_t(2) * QROWS * (TILE + 8) * 2 + 4 * QROWS * 4 +
          4 * QROWS * 8;
 }
 
