@@ -350,6 +350,13 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
     if (c < nchunks) accum(keep[i]);
   }
   for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum(xr[c]);
+  // The row stays in registers in its storage type: an empty asm "changing"
+  // it keeps the compiler from holding every element's fp32 widening (twice
+  // the registers) from the sum until the output pass.
+  if constexpr (VEC > 1) {
+#pragma unroll
+    for (int i = 0; i < NREG; ++i) asm volatile("" : "+v"(keep[i].v));
+  }
   const uint64_t total = block_sat_sum(static_cast<uint64_t>(acc), qmax, ired);
 
   const float lnS = total == 0 ? -__builtin_inff()
