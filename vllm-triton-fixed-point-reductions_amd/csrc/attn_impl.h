@@ -728,6 +728,64 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   const ConstI32Ptr bt_row = (ConstI32Ptr)(a.bt + int64_t(r) * a.sbt);
   const int last_block = int(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
 
+  // DMA of tile t (K or V) into stage buf: the wave moves key rows
+  // 16 wave .. 16 wave + 15 (one page), instruction q rows 16 wave + q*KPI
+  // .. +KPI-1, lane l row +l/CPR, slot l%CPR, i.e. chunk slot ^ swz(row).
+  const T* Kc = static_cast<const T*>(a.k);
+  const T* Vc = static_cast<const T*>(a.v);
+  auto page_entry = [&](int t) -> int {  // the wave's page of tile t (keys clamped)
+    const int key0 = min(t * TILE + 16 * wave, seq_len - 1);
+    const int lb = __builtin_amdgcn_readfirstlane(key0 >> a.ps_shift);
+    return bt_row[min(lb, a.max_blocks - 1)];
+  };
+  auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
+    const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
+#pragma unroll
+    for (int q = 0; q < G::NDMA; ++q) {
+      const int row0q = 16 * wave + q * G::KPI;
+      const int rr = row0q + lane / G::CPR;
+      const int key = min(t * TILE + rr, seq_len - 1);
+      const int c = (lane % G::CPR) ^ G::swz(rr);
+      const int64_t sb = isv ? a.sv_b : a.sk_b, ss = isv ? a.sv_s : a.sk_s, sh = isv ? a.sv_h : a.sk_h;
+      const uint64_t off = uint64_t(p) * uint32_t(sb) + uint64_t(uint32_t(key & (a.page_size - 1))) * uint32_t(ss) +
+                           uint64_t(uint32_t(g)) * uint32_t(sh) + uint32_t(c * 8);
+      const T* src = (isv ? Vc : Kc) + off;
+      const unsigned dst = lds0 + buf * G::TILEB + row0q * G::ROWB;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
+    }
+  };
+
+  // The first NS - 1 steps' DMAs go out before the Q and row-setup loads,
+  // so their latencies overlap; one wait covers both before the first step.
+  auto live_lo = [&](int cc) { return max(cc * CT, t_lo); };
+  auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
+  // the step after (cc, isv, t)
+  auto advance = [&](int& cc, bool& isv, int& t) {
+    if (++t < live_hi(cc)) return;
+    if (!isv) {
+      isv = true;
+      t = live_lo(cc);
+    } else if (cc + 1 < my_hi) {
+      ++cc;
+      isv = false;
+      t = live_lo(cc);
+    } else {
+      t = live_hi(cc) - 1;  // past the end: re-issue the last tile
+    }
+  };
+  int dc_ = my_lo, dt = my_lo < my_hi ? live_lo(my_lo) : 0;  // DMA cursor
+  bool dv = false;
+  int dent = 0;  // page entry at the cursor
+  if (my_lo < my_hi) {
+    dent = page_entry(dt);
+#pragma unroll
+    for (int i = 0; i + 1 < NS; ++i) {
+      dma_tile(dv, dt, dent, i);
+      advance(dc_, dv, dt);
+      dent = page_entry(dt);
+    }
+  }
+
   // Q fragments (MFMA A operand): lane holds row lane%16, its k slots.
   u32x4 qf[QSTEPS];
   {
@@ -759,6 +817,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
     }
   }
 
+  // Q, row setup and the first DMAs landed (an s_waitcnt the compiler sees,
+  // so it does not wait for the setup loads later behind the loop's DMAs).
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+
   // Per-lane LDS offsets within a stage.
   // K fragment j of the lane's key (row wave*16 + lane%16), chunk 4j + kg.
   unsigned koff[QSTEPS];
@@ -784,33 +846,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
         voff[b][s][h] = rr * G::ROWB + ((c ^ G::swz(rr)) << 4) + (j & 1) * 8;
       }
 
-  // DMA of tile t (K or V) into stage buf: the wave moves key rows
-  // 16 wave .. 16 wave + 15 (one page), instruction q rows 16 wave + q*KPI
-  // .. +KPI-1, lane l row +l/CPR, slot l%CPR, i.e. chunk slot ^ swz(row).
-  const T* Kc = static_cast<const T*>(a.k);
-  const T* Vc = static_cast<const T*>(a.v);
-  auto page_entry = [&](int t) -> int {  // the wave's page of tile t (keys clamped)
-    const int key0 = min(t * TILE + 16 * wave, seq_len - 1);
-    const int lb = __builtin_amdgcn_readfirstlane(key0 >> a.ps_shift);
-    return bt_row[min(lb, a.max_blocks - 1)];
-  };
-  auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
-    const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
-#pragma unroll
-    for (int q = 0; q < G::NDMA; ++q) {
-      const int row0q = 16 * wave + q * G::KPI;
-      const int rr = row0q + lane / G::CPR;
-      const int key = min(t * TILE + rr, seq_len - 1);
-      const int c = (lane % G::CPR) ^ G::swz(rr);
-      const int64_t sb = isv ? a.sv_b : a.sk_b, ss = isv ? a.sv_s : a.sk_s, sh = isv ? a.sv_h : a.sk_h;
-      const uint64_t off = uint64_t(p) * uint32_t(sb) + uint64_t(uint32_t(key & (a.page_size - 1))) * uint32_t(ss) +
-                           uint64_t(uint32_t(g)) * uint32_t(sh) + uint32_t(c * 8);
-      const T* src = (isv ? Vc : Kc) + off;
-      const unsigned dst = lds0 + buf * G::TILEB + row0q * G::ROWB;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
-    }
-  };
-
   float Mr[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
   AccT Dr[4] = {0, 0, 0, 0};
   AccT Wr[DB_PER_WAVE][4];
@@ -824,34 +859,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
     // stage s % NS; its DMAs were issued NS - 1 steps earlier (past the last
     // step the last tile is re-issued into the free stage, so every step
     // issues the same number of DMAs and the wait count stays exact).
-    auto live_lo = [&](int cc) { return max(cc * CT, t_lo); };
-    auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
-    // the step after (cc, isv, t)
-    auto advance = [&](int& cc, bool& isv, int& t) {
-      if (++t < live_hi(cc)) return;
-      if (!isv) {
-        isv = true;
-        t = live_lo(cc);
-      } else if (cc + 1 < my_hi) {
-        ++cc;
-        isv = false;
-        t = live_lo(cc);
-      } else {
-        t = live_hi(cc) - 1;  // past the end: re-issue the last tile
-      }
-    };
-    // The Q and row-setup loads land first (an s_waitcnt the compiler sees,
-    // so it does not later wait for them behind the DMAs).
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    int dc_ = my_lo, dt = live_lo(my_lo);  // DMA cursor
-    bool dv = false;
-    int dent = page_entry(dt);  // page entry at the cursor
-#pragma unroll
-    for (int i = 0; i + 1 < NS; ++i) {
-      dma_tile(dv, dt, dent, i);
-      advance(dc_, dv, dt);
-      dent = page_entry(dt);
-    }
 
     float sc[CT][4];
     float mx[4];
