@@ -126,6 +126,79 @@ def test_gemm_deterministic_across_runs():
         assert torch.equal(r0, KG.gemm_fxp_run(a, b, None, 32, 16))
 
 
+# --- large-M kernel: rounding-constant quantisation and its exact fallback ---
+# gemm_big_kernel (16-bit inputs, M > 64, K-contiguous B) quantises a wave's
+# K-tile by the rounding constant 1.5 * 2^23 when every partial satisfies
+# |P| < 2^22 / 2^f (32767 / 2^f for 16-bit accumulators), and exactly
+# otherwise. Inputs below keep every K-tile dot exact in fp32, so the result
+# must equal the oracle bit for bit on either path.
+
+_BIG_M = [256, 1024]  # 8-wave 256 x 128 tiles below M = 1024, 4-wave 128 x 128 from there
+
+
+def _dyadic(shape, lo, hi, exp2, g, dtype):
+    return (torch.randint(lo, hi + 1, shape, generator=g).double() * 2.0 ** exp2).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", _BIG_M)
+@pytest.mark.parametrize("bits,frac", [(32, 16), (16, 8), (32, 8), (16, 12)])
+@pytest.mark.parametrize("K", [384, 300])
+def test_gemm_big_rounding_constant_ties(dtype, M, bits, frac, K):
+    # products are multiples of 2^-(f+1): many partials lie exactly halfway
+    # between two fixed-point steps (round half to even), all far inside the
+    # fast range; K = 300 adds the peeled partial last K-tile
+    g = torch.Generator("cpu").manual_seed(M + frac + K)
+    u = (frac + 1) // 2
+    a = _dyadic((M, K), -8, 8, -u, g, dtype)
+    b = _dyadic((K, 256), -8, 8, -(frac + 1 - u), g, dtype)
+    got = _run(a, b, bits=bits, frac=frac, b_layout="nk")
+    want = _oracle(a, b, None, bits, frac)
+    assert torch.equal(got, want), mismatch_report(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", _BIG_M)
+def test_gemm_big_mixed_tile_paths(dtype, M):
+    # some waves' K-tiles hold partials beyond the fast range (|P| up to 2048
+    # against 64 at Q16): those tiles take the exact path, the wave's other
+    # tiles and the other waves the rounding constant
+    g = torch.Generator("cpu").manual_seed(11 + M)
+    K, N = 512, 256
+    a = _dyadic((M, K), -2, 2, -6, g, dtype)
+    b = _dyadic((K, N), -2, 2, 0, g, dtype)
+    a[64:128, 128:256] *= 256  # one wave row, second K-tile
+    a[M - 64:M - 48, 384:512] *= 256  # 16 rows of one wave, last K-tile
+    a[3, 0:128] *= 256  # a single row, first K-tile
+    for bits in (32, 16):
+        frac = 16 if bits == 32 else 8
+        got = _run(a, b, bits=bits, frac=frac, b_layout="nk")
+        want = _oracle(a, b, None, bits, frac)
+        assert torch.equal(got, want), (bits, mismatch_report(got, want))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", _BIG_M)
+def test_gemm_big_nonfinite_partials(dtype, M):
+    # NaN and infinite partials fail the range check (the exact path turns
+    # NaN into 0 and saturates infinities); the rest of their waves' tiles
+    # are unaffected
+    g = torch.Generator("cpu").manual_seed(5 + M)
+    K, N = 384, 256
+    a = _dyadic((M, K), -2, 2, -4, g, dtype)
+    b = _dyadic((K, N), -2, 2, 0, g, dtype)
+    a[5, 10] = float("inf")
+    a[70, 300] = float("-inf")
+    a[130, 200] = float("nan")
+    b[17, 9] = float("nan")
+    if dtype == torch.bfloat16:
+        a[200, 140] = 2.0 ** 100  # finite inputs whose products overflow fp32
+        b[140, :] = b[140, :] * 2.0 ** 30
+    got = _run(a, b, bits=32, frac=16, b_layout="nk")
+    want = _oracle(a, b, None, 32, 16)
+    assert torch.equal(got, want), mismatch_report(got, want)
+
+
 # --- restated reference tests (fxpr_vllm/_tests/test_gemm.py) ---------------
 
 @pytest.mark.parametrize("M,N,K", [(4, 4, 16), (3, 7, 16), (1, 1, 32), (8, 16, 32)])

@@ -61,6 +61,19 @@ def _run(cmd: list[str], verbose: bool) -> None:
             print(line)
 
 
+def _check_defined(lib: Path) -> None:
+    """Fail if the library references a symbol of its own namespace that no
+    object defines (a kernel whose host launch stub was not emitted links
+    fine and fails only at load time)."""
+    nm = shutil.which("nm")
+    if nm is None:
+        return
+    res = subprocess.run([nm, "-D", "--undefined-only", str(lib)], capture_output=True, text=True)
+    missing = [ln.split()[-1] for ln in res.stdout.splitlines() if "4fxpr" in ln]
+    if missing:
+        raise RuntimeError(f"{lib.name}: undefined symbols of the library's own code: {missing[:4]}")
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
@@ -79,6 +92,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     tmp = OUT.with_suffix(".so.tmp")
     _run([cc, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp)],
          verbose)
+    _check_defined(tmp)
     os.replace(tmp, OUT)
     return OUT
 

@@ -79,6 +79,10 @@ struct GemmArgs {
   int64_t ldb;       // B: stride between n columns (K-contiguous) or k rows (N-contiguous)
   int64_t scm, scn;  // C strides
   float scale, inv_scale;
+  // A K-tile whose partials all satisfy |P| < fast_lim (0: never) quantises
+  // by the rounding constant (gemm_big_kernel): scale is 2^f with f >= 0 and
+  // fast_lim * scale <= 2^22 (32767 for 16-bit accumulators).
+  float fast_lim;
   int ktiles, tiles_per_split, tiles_m, tiles_n;
   int c_vec;         // C rows unit-stride, 16-byte aligned (vector row stores)
 };
@@ -407,6 +411,22 @@ template <class BT> constexpr size_t big_lds_bytes() {
 }
 
 typedef __attribute__((address_space(3))) void* LdsPtr;
+// Buffer resource word 3 for raw (unformatted, unswizzled) buffer access on
+// gfx9-family parts.
+constexpr int kBufferDword3 = 0x00020000;
+// 16 bytes per lane from a raw buffer into LDS at dst + 16 * lane. (A helper:
+// called directly in a kernel template, the builtin makes the host pass drop
+// the kernel's launch stub.)
+__device__ __forceinline__ void buffer_to_lds(__amdgpu_buffer_rsrc_t r, unsigned dst, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)(uintptr_t)dst, 16, voff, soff, 0, 0);
+}
+// A pointer the caller knows to be wave-uniform, as scalar registers (buffer
+// resources must be).
+template <typename T> __device__ __forceinline__ void* uniform_ptr(const T* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(u)), hi = __builtin_amdgcn_readfirstlane(uint32_t(u >> 32));
+  return reinterpret_cast<void*>((uint64_t(hi) << 32) | lo);
+}
 
 template <int DT, int BITS, class BT, bool SPLIT>
 __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs args) {
@@ -428,7 +448,8 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
 
   const T* A = static_cast<const T*>(args.a);
   const T* B = static_cast<const T*>(args.b);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS targets in SGPRs
   const int wm = wave / BT::WGN, wn = wave % BT::WGN;
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, tm, tn);
@@ -443,30 +464,32 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
   // DMA sources. Instruction q of this wave covers rows 8 i .. 8 i + 7 of
   // the A (B) stage, i = wave + NW q; lane l brings row 8 i + l / 8, chunk
   // (l % 8) ^ ((row >> 1) & 7). Rows past M / N are clamped: they feed only
-  // outputs that are never stored.
-  const T* src[NDMA];
+  // outputs that are never stored. Buffer loads: a resource per matrix based
+  // at the tile's first row and k = kb0, a fixed 32-bit lane offset (the host
+  // keeps BM * ld * 2 bytes below 2^31; no range limit) and the stage offset in
+  // a scalar.
+  const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(A + m0 * args.lda + kb0), short(0), -1, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(B + n0 * args.ldb + kb0), short(0), -1, kBufferDword3);
+  uint32_t voff[NDMA];
 #pragma unroll
   for (int q = 0; q < NDMA; ++q) {
     const bool isa = q < NIA;
     const int i = wave + NW * (isa ? q : q - NIA);
     const int r = 8 * i + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    if (isa) {
-      const int64_t m = min<int64_t>(m0 + r, args.M - 1);
-      src[q] = A + m * args.lda + kb0 + c * CH;
-    } else {
-      const int64_t n = min<int64_t>(n0 + r, args.N - 1);
-      src[q] = B + n * args.ldb + kb0 + c * CH;
-    }
+    const int64_t row = isa ? min<int64_t>(m0 + r, args.M - 1) - m0 : min<int64_t>(n0 + r, args.N - 1) - n0;
+    voff[q] = uint32_t((row * (isa ? args.lda : args.ldb) + c * CH) * int64_t(sizeof(T)));
   }
   auto dma = [&](int s, int buf) {  // stage s (64 k from kb0) into LDS buffer buf
+    const int soff = s * (BKS * int(sizeof(T)));
 #pragma unroll
     for (int q = 0; q < NDMA; ++q) {
       const bool isa = q < NIA;
       const int i = wave + NW * (isa ? q : q - NIA);
       const unsigned dst = lds0 + buf * STAGE + (isa ? 0 : BM * 128) + i * 1024;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src[q] + int64_t(s) * BKS),
-                                       (LdsPtr)(uintptr_t)dst, 16, 0, 0);
+      buffer_to_lds(isa ? arsrc : brsrc, dst, voff[q], soff);
     }
   };
 
@@ -517,7 +540,57 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
   };
   auto quantize_block = [&](int i, int j) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) I[i][j][r] = wrap_add<BITS>(I[i][j][r], quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
+    for (int r = 0; r < 4; ++r) {
+      if constexpr (BITS == 64) {
+        I[i][j][r] = wrap_add<BITS>(I[i][j][r], quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
+      } else {
+        // the accumulator updated in place, as in quantize_block_fast: the
+        // two paths then meet without register copies
+        const int32_t q = static_cast<int32_t>(quant<BITS>(__fmul_rn(P[i][j][r], args.scale)));
+        asm("v_add_u32 %0, %0, %1" : "+v"(I[i][j][r]) : "v"(q));
+      }
+    }
+  };
+  // Rounding-constant quantisation, for a K-tile whose partials all satisfy
+  // |P| < fast_lim (so |P * 2^f| < 2^22, exact): fl32(x + 1.5 * 2^23) is
+  // RNE(x) + 1.5 * 2^23 (the sum lies in [2^23, 2^24), where the spacing is
+  // 1, and the constant is even, so a tie goes to the same even integer), and
+  // its bit pattern minus the constant's is RNE(x). No saturation can occur.
+  // Same bits as quantize_block; two instructions per element instead of four.
+  // (The accumulator update is written as an instruction: from C the
+  // compiler splits the add off into extra moves and adds.)
+  const float magic = 12582912.0f;  // 1.5 * 2^23, bit pattern 0x4B400000
+  const uint32_t neg_magic_bits = 0xB4C00000u;  // -0x4B400000 mod 2^32
+  auto quantize_block_fast = [&](int i, int j) {
+    if constexpr (BITS != 64) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float y = __builtin_fmaf(P[i][j][r], args.scale, magic);
+        asm("v_add3_u32 %0, %0, %1, %2" : "+v"(I[i][j][r]) : "v"(y), "v"(neg_magic_bits));
+      }
+    }
+  };
+  // Whether every partial of the wave's tile satisfies |P| < fast_lim (NaN
+  // and infinities fail: v_maximum3_f32 propagates NaN).
+  auto tile_fast = [&]() -> bool {
+    if constexpr (BITS == 64) {
+      return false;
+    } else {
+      float m[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; j += 2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            asm("v_maximum3_f32 %0, |%1|, |%2|, %3"
+                : "=v"(m[r])
+                : "v"(P[i][j][r]), "v"(P[i][j + 1][r]), "v"(m[r]));
+      float mm;
+      asm("v_maximum3_f32 %0, %1, %2, %3" : "=v"(mm) : "v"(m[0]), "v"(m[1]), "v"(m[2]));
+      asm("v_maximum3_f32 %0, %1, %2, %2" : "=v"(mm) : "v"(mm), "v"(m[3]));
+      return __builtin_amdgcn_ballot_w64(!(mm < args.fast_lim)) == 0;
+    }
   };
   auto quantize = [&]() {
 #pragma unroll
@@ -589,7 +662,12 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA * (NS - 2)) : "memory");
     __builtin_amdgcn_s_barrier();
     read_frags(0, 0, fa0, fb0);
-    auto stage = [&](int s, bool tile_start) {
+    // tile_start: quantise the previous K-tile's partials block by block.
+    // 16- and 32-bit accumulators: by the rounding constant (a K-tile that
+    // fails tile_fast was quantised exactly beforehand and its partials set
+    // to zero, which the rounding constant turns into zero); 64-bit: exactly.
+    auto stage = [&](int s, auto tile_start_tag) {
+      constexpr bool tile_start = decltype(tile_start_tag)::value;
       const int buf = s % NS;
       dma(min(s + NS - 1, nst - 1), (s + NS - 1) % NS);
       lds_wait(fa0, fb0);
@@ -598,7 +676,12 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
 #pragma unroll
       for (int b = 0; b < MB * NB; ++b) {
         const int i = b / NB, j = b % NB;
-        if (tile_start) quantize_block(i, j);
+        if constexpr (tile_start) {
+          if constexpr (BITS == 64)
+            quantize_block(i, j);
+          else
+            quantize_block_fast(i, j);
+        }
         mma(i, j, fa0[i], fb0[j], tile_start);
         switch (b) {
           case 0: read_frag(aa1, fa1[0], std::integral_constant<int, 0>{}); break;
@@ -628,8 +711,17 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       read_frags((s + 1) % NS, 0, fa0, fb0);
     };
     for (int s = 0; s < nst; s += 2) {
-      stage(s, true);
-      stage(s + 1, false);
+      if constexpr (BITS != 64) {
+        if (!tile_fast()) {  // rare: partials out of the fast range, NaN or infinite
+          quantize();
+#pragma unroll
+          for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) P[i][j] = zero4;
+        }
+      }
+      stage(s, std::true_type{});
+      stage(s + 1, std::false_type{});
     }
     lds_wait(fa0, fb0);                               // trailing reads (unused)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing DMAs into unused buffers
@@ -794,11 +886,14 @@ inline void tile_dims(TileId t, int& bm, int& bn) {
 template <int DT, int BITS>
 int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
   const TileId t = pick_tile(a.M);
+  // gemm_big_kernel's 32-bit lane offsets span up to 256 rows of A or B
+  const bool big_ok = vec && !b_ncontig && t == TileId::Big && a.lda <= (int64_t(1) << 22) &&
+                      a.ldb <= (int64_t(1) << 22);
   if constexpr (DT != FXPR_DTYPE_F32 && BITS == 64) {
-    if (vec && !b_ncontig && t == TileId::Big) return launch_big<DT, BITS, TB64>(a, splits, st);
+    if (big_ok) return launch_big<DT, BITS, TB64>(a, splits, st);
   }
   if constexpr (DT != FXPR_DTYPE_F32 && BITS != 64) {
-    if (vec && !b_ncontig && t == TileId::Big) {
+    if (big_ok) {
       // two 4-wave workgroups per CU from M = 1024 (6 % faster at M = 8192),
       // one 8-wave workgroup below (fewer, larger tiles while HBM-bound)
       if (a.M >= 1024) return launch_big<DT, BITS, TB2>(a, splits, st);
