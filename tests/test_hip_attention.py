@@ -370,6 +370,24 @@ def test_prefill_workgroups_formats_windows_alibi_softcap(bits, frac):
                              window=333), tol)
 
 
+@pytest.mark.parametrize("bits,frac", [(16, 8), (32, 16), (32, 32), (64, 32)])
+@pytest.mark.parametrize("window", [0, 333])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_prefill_score_variants_match_split_path(bits, frac, window, sign):
+    # the prefill workgroups' fast variant (no softcap / ALiBi, positive
+    # scale, 2^f within the rounding constant's range: (16, 8) and (32, 16);
+    # whole tiles unmasked, the row maximum taken before scaling) and their
+    # general one ((32, 32), (64, 32), a negative scale) against the split
+    # path, bit for bit, with NaN keys in one request
+    dtype = torch.bfloat16
+    q, kv, qsl, sl, bt = _prefix_case([260, 140], [600, 50], 8, 2, 128, 16, dtype, seed=bits + frac)
+    kv[bt[0, 5].long(), 0, 3, 1, 7] = float("nan")  # key 83 of request 0, kv head 1
+    kw = dict(scale=sign / math.sqrt(128), bits=bits, frac=frac, window=window)
+    one = attend(q, kv, qsl, sl, bt, 260, 1, **kw)
+    split = attend(q, kv, qsl, sl, bt, 260, 4, **kw)
+    assert torch.equal(one.view(torch.int16), split.view(torch.int16))
+
+
 def test_prefill_rows_equal_their_decode_step():
     # the last prompt token computed inside a 400-token prefill equals the
     # same token computed as a one-token decode over the cached prefix

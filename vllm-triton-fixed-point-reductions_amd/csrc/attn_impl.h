@@ -1383,6 +1383,431 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_kernel(AttnArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill workgroups fed by LDS DMA (16-bit inputs, rows exactly DMAX wide,
+// pages of 16 keys or more): attn_prefill_kernel's rows, chunk statistics and
+// bits, with the tiles brought into an NS-stage LDS ring by global_load_lds
+// NS - 1 steps ahead (one scalar page-entry load per wave and tile) instead
+// of register-staged loads one step ahead. A tile occupies one stage (its
+// 64 key rows, 16-byte chunk c of row r at slot c ^ swz(r), as in
+// attn_dma_kernel). Steps per chunk: its live K tiles (row maxima), then per
+// live tile its K tile (weights, denominators, the wave's P) and its V tile
+// (weighted V); one tile and one barrier per step. All LDS accesses of the
+// loop are inline asm with explicit waits (the compiler would otherwise wait
+// for every DMA in flight before each of them).
+template <int DMAX> struct PDmaGeom {
+  static constexpr int ROWB = DMAX * 2;              // bytes per key row
+  static constexpr int CPR = ROWB / 16;              // 16-byte chunks per row
+  static constexpr int KPI = 1024 / ROWB;            // key rows per wave instruction
+  static constexpr int TILEB = TILE * ROWB;          // bytes per tile
+  static constexpr int RPW = TILE / PQ_WAVES;        // key rows each wave moves per tile
+  static constexpr int NDMA = RPW / KPI;             // DMA instructions per wave per tile
+  static constexpr int NS = 8;                       // LDS stages
+  static_assert(NDMA >= 1 && NDMA * KPI == RPW, "tile rows per wave");
+};
+
+template <int DMAX> constexpr size_t prefill_dma_lds_bytes() {
+  return size_t(PDmaGeom<DMAX>::NS) * PDmaGeom<DMAX>::TILEB + size_t(PQ_WAVES) * 16 * (TILE + 8) * 2;
+}
+
+__device__ __forceinline__ void lds_write_b16_hi(unsigned addr, uint32_t x) {
+  asm volatile("ds_write_b16_d16_hi %0, %1" ::"v"(addr), "v"(x) : "memory");
+}
+// Two weights as 16-bit values (RNE) in one register, low half first; NaN
+// payloads as the conversion leaves them.
+template <int DT> __device__ __forceinline__ uint32_t p_pack2(float lo, float hi) {
+  if constexpr (DT == FXPR_DTYPE_BF16) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t v = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+template <int OFF> __device__ __forceinline__ void lds_read_b128_off(unsigned addr, u32x4& x) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(addr), "n"(OFF) : "memory");
+}
+
+template <int DT, int BITS, int DMAX>
+__global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs a) {
+  static_assert(DT != FXPR_DTYPE_F32, "16-bit inputs only");
+  using TR = Traits<DT>;
+  using T = typename TR::T;
+  using AccT = typename AccOf<BITS>::T;
+  using G = PDmaGeom<DMAX>;
+  using SW = DmaGeom<DMAX>;  // the row swizzle
+  constexpr int KI = TR::KI, QUNIT = TR::QUNIT;
+  constexpr int QSTEPS = DMAX / KI;
+  constexpr int DBLK = DMAX / 16;
+  constexpr int NK0 = QUNIT / KI;  // MFMA k steps per quantised chain
+  constexpr int VP = TILE + 8;     // Ps row pitch (elements)
+  constexpr int NS = G::NS;
+  constexpr int PS_OFF = NS * G::TILEB;
+  static_assert(TILE == QUNIT, "one quantised chain per tile");
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(smem_raw));
+
+  const int tid = threadIdx.x, lane = tid & 63, kg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = blockIdx.x / a.num_kv_heads, g = blockIdx.x % a.num_kv_heads;
+  const int q_start = a.qsl[r];
+  const int q_len = a.qsl[r + 1] - q_start;
+  const int seq_len = a.seq_lens[r];
+  const int ctx = seq_len - q_len;
+  const int rows_total = q_len * a.group;
+  const int row0 = blockIdx.y * PQROWS;
+  if (row0 >= rows_total || rows_total < a.pq_rows) return;  // uniform; short requests: the 16-row kernels
+  const int wrow0 = row0 + 16 * wave;
+
+  const int i_min = row0 / a.group;
+  const int i_max = min(rows_total - 1, row0 + PQROWS - 1) / a.group;
+  const int hi = a.causal ? min(seq_len, ctx + i_max + 1) : seq_len;
+  const int lo = a.window > 0 ? max(0, ctx + i_min - a.window + 1) : 0;
+  const int t_lo = lo / TILE;
+  const int t_hi = hi > lo ? (hi + TILE - 1) / TILE : t_lo;
+  const int c_lo = t_lo / CT;
+  const int c_hi = t_hi > t_lo ? (t_hi + CT - 1) / CT : c_lo;
+
+  const ConstI32Ptr bt_row = (ConstI32Ptr)(a.bt + int64_t(r) * a.sbt);
+  const int last_block = int(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
+  const T* Kc = static_cast<const T*>(a.k);
+  const T* Vc = static_cast<const T*>(a.v);
+  // The wave moves key rows RPW wave .. RPW wave + RPW - 1 of a tile (within
+  // one page: pages hold 16 keys or more); instruction q rows RPW wave +
+  // q KPI .., lane l row + l / CPR, chunk slot l % CPR, i.e. chunk
+  // (l % CPR) ^ swz(row). Keys past the sequence are clamped (their scores
+  // are masked).
+  auto page_entry = [&](int t) -> int {
+    const int key0 = min(t * TILE + G::RPW * wave, seq_len - 1);
+    const int lb = __builtin_amdgcn_readfirstlane(key0 >> a.ps_shift);
+    return bt_row[min(lb, a.max_blocks - 1)];
+  };
+  auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
+    const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
+#pragma unroll
+    for (int q = 0; q < G::NDMA; ++q) {
+      const int row0q = G::RPW * wave + q * G::KPI;
+      const int rr = row0q + lane / G::CPR;
+      const int key = min(t * TILE + rr, seq_len - 1);
+      const int c = (lane % G::CPR) ^ SW::swz(rr);
+      const int64_t sb = isv ? a.sv_b : a.sk_b, ss = isv ? a.sv_s : a.sk_s, sh = isv ? a.sv_h : a.sk_h;
+      const uint64_t off = uint64_t(p) * uint32_t(sb) + uint64_t(uint32_t(key & (a.page_size - 1))) * uint32_t(ss) +
+                           uint64_t(uint32_t(g)) * uint32_t(sh) + uint32_t(c * 8);
+      const T* src = (isv ? Vc : Kc) + off;
+      const unsigned dst = lds0 + buf * G::TILEB + row0q * G::ROWB;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
+    }
+  };
+
+  // The tile stream: per chunk cc, its nt live K tiles (phase 0), then K and
+  // V of each live tile in turn (phase 1, 2 nt entries). The DMA cursor runs
+  // NS - 1 entries ahead; past the end it re-issues the last entry into the
+  // free stage, so every step issues the same DMAs and the wait count stays
+  // exact. The first entries go out before the Q and row-setup loads.
+  auto live_lo = [&](int cc) { return max(cc * CT, t_lo); };
+  auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
+  int dcc = c_lo, dph = 0, didx = 0;  // DMA cursor
+  auto cur_tile = [&]() { return live_lo(dcc) + (dph ? (didx >> 1) : didx); };
+  auto cur_isv = [&]() { return dph == 1 && (didx & 1); };
+  auto advance = [&]() {
+    const int nt = live_hi(dcc) - live_lo(dcc);
+    if (++didx < (dph ? 2 * nt : nt)) return;
+    if (dph == 0) {
+      dph = 1;
+      didx = 0;
+    } else if (dcc + 1 < c_hi) {
+      ++dcc;
+      dph = 0;
+      didx = 0;
+    } else {
+      didx = 2 * nt - 1;
+    }
+  };
+  int dent = 0;
+  if (c_lo < c_hi) {
+    dent = page_entry(cur_tile());
+#pragma unroll
+    for (int i = 0; i + 1 < NS; ++i) {
+      dma_tile(cur_isv(), cur_tile(), dent, i);
+      advance();
+      dent = page_entry(cur_tile());
+    }
+  }
+
+  // Q fragments of the wave's rows (MFMA A operand: row lane%16, k slots kg).
+  u32x4 qf[QSTEPS];
+  {
+    const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + (lane & 15));
+    const T* qbase = static_cast<const T*>(a.q) + qrow.token * a.sq_t + int64_t(qrow.head) * a.sq_h;
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) {
+      const int d = 32 * j + 8 * kg;
+      qf[j] = qrow.valid ? *reinterpret_cast<const u32x4*>(qbase + d) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // Rows of the score / PV layout: the wave's rows 4*kg + e.
+  int ks[4], ke[4], qp[4];
+  float slope[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + 4 * kg + e);
+    ks[e] = ri.valid ? ri.kstart : 0x7fffffff;
+    ke[e] = ri.valid ? ri.kend : 0;
+    qp[e] = ri.qpos;
+    slope[e] = a.alibi ? a.alibi[ri.head] : 0.0f;
+  }
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): Q, row setup and the first DMAs
+
+  // Per-lane LDS offsets within a stage. K fragment j of key row kb*16 +
+  // lane%16: chunk 4j + kg (the swizzle depends on the row's low four bits
+  // only, so key block kb adds kb * 16 rows). V B-operand reads
+  // (ds_read_b64_tr_b16) of d block db: keys s*KI + 8kg + (j>>2) (+4 for the
+  // upper half), columns db*16 + 4*(j&3), j = lane%16.
+  unsigned koff[QSTEPS];
+#pragma unroll
+  for (int j = 0; j < QSTEPS; ++j) {
+    const int rr = lane & 15;
+    koff[j] = rr * G::ROWB + (((4 * j + kg) ^ SW::swz(rr)) << 4);
+  }
+  unsigned voff[DBLK][NK0][2];
+#pragma unroll
+  for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+    for (int s = 0; s < NK0; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = lane & 15;
+        const int rr = s * KI + 8 * kg + (j >> 2) + 4 * h;
+        const int c = 2 * db + ((j & 3) >> 1);
+        voff[db][s][h] = rr * G::ROWB + ((c ^ SW::swz(rr)) << 4) + (j & 1) * 8;
+      }
+  const unsigned ps_w = lds0 + PS_OFF + wave * 16 * VP * 2;  // the wave's P [16][VP]
+
+  float Mr[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  AccT Dr[4] = {0, 0, 0, 0};
+  AccT Wr[DBLK][4];
+#pragma unroll
+  for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Wr[b][e] = 0;
+
+  // Fast variant (same bits): no softcap or ALiBi and a positive scale, so a
+  // score is fl(acc * scale) and the chunk maximum is fl(max(acc) * scale)
+  // (rounding is monotone); tiles every row of the wave sees whole skip the
+  // mask; a weight w in [0, 1] quantises by the rounding constant (2^f within
+  // its range, see fast_den); P is stored without the canonical-NaN rule (any
+  // NaN weight yields a NaN weighted V either way, which quantises to 0).
+  const bool fast_den = BITS != 64 && a.fxp_scale <= (BITS == 16 ? 16384.0f : 4194304.0f);
+  const bool fast = fast_den && !(a.softcap_log2 > 0.0f) && !a.alibi && a.scale_log2 > 0.0f;
+  auto run = [&](auto fast_tag) __attribute__((always_inline)) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    int step = 0;
+    auto step_begin = [&]() -> unsigned {
+      // own DMAs of this step landed (only later steps' in flight), own LDS
+      // accesses done; the barrier makes both everyone's
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(G::NDMA * (NS - 2)) : "memory");
+      __builtin_amdgcn_s_barrier();
+      dma_tile(cur_isv(), cur_tile(), dent, (step + NS - 1) % NS);
+      advance();
+      dent = page_entry(cur_tile());
+      const unsigned base = lds0 + (step % NS) * G::TILEB;
+      ++step;
+      return base;
+    };
+    // acc = the MFMA chain of key block kb of the tile at base, as in attn_kernel
+    auto block_acc = [&](unsigned base, auto kbc) __attribute__((always_inline)) -> f32x4 {
+      constexpr int kb = decltype(kbc)::value;
+      u32x4 kf[QSTEPS];
+      static_for<QSTEPS>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        lds_read_b128_off<kb * 16 * G::ROWB>(base + koff[j], kf[j]);
+      });
+      if constexpr (QSTEPS == 4) lds_wait_for(kf[0], kf[1], kf[2], kf[3]);
+      else lds_wait_for(kf[0], kf[1]);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < QSTEPS; ++j) acc = TR::mma(qf[j], kf[j], acc);
+      return acc;
+    };
+    // Scores of key block kb of tile t for the lane's rows (attn_kernel's
+    // post-processing); whole: every row of the wave sees the whole tile.
+    auto block_scores = [&](const f32x4& acc, int t, int kb, bool whole, float (&sc)[4]) __attribute__((always_inline)) {
+      const int key = t * TILE + kb * 16 + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x = __fmul_rn(acc[e], a.scale_log2);
+        if constexpr (!FAST) {
+          if (a.softcap_log2 > 0.0f) x = a.softcap_log2 * tanh_approx(x / a.softcap_log2);
+          if (a.alibi) x = x + slope[e] * static_cast<float>(key - qp[e]);
+        }
+        sc[e] = (whole || (key >= ks[e] && key < ke[e])) ? x : -__builtin_inff();
+      }
+    };
+    auto tile_whole = [&](int t) -> bool {
+      bool out = false;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out = out || !(ks[e] <= t * TILE && t * TILE + TILE <= ke[e]);
+      return __builtin_amdgcn_ballot_w64(out) == 0;
+    };
+
+    for (int c = c_lo; c < c_hi; ++c) {
+      const int ta = live_lo(c), te = live_hi(c);
+      float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+      float mraw[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+      // phase 0: the chunk's row maxima
+      for (int t = ta; t < te; ++t) {
+        const unsigned base = step_begin();
+        if (FAST && tile_whole(t)) {
+          static_for<TILE / 16>([&](auto kbc) {
+            const f32x4 acc = block_acc(base, kbc);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mraw[e] = fmaxf(mraw[e], acc[e]);
+            __builtin_amdgcn_sched_barrier(0);
+          });
+        } else {
+          static_for<TILE / 16>([&](auto kbc) {
+            const f32x4 acc = block_acc(base, kbc);
+            float sc[4];
+            block_scores(acc, t, decltype(kbc)::value, false, sc);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], sc[e]);
+            __builtin_amdgcn_sched_barrier(0);
+          });
+        }
+      }
+      float m[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (FAST) mx[e] = fmaxf(mx[e], __fmul_rn(mraw[e], a.scale_log2));
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o, 64));
+        m[e] = mx[e] != -__builtin_inff() ? mx[e] : 0.0f;  // no key: pin to 0
+      }
+      // phase 1: weights and weighted V, tile by tile
+      AccT den[4] = {0, 0, 0, 0};
+      AccT wv[DBLK][4];
+#pragma unroll
+      for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[b][e] = 0;
+      for (int t = ta; t < te; ++t) {
+        {
+          const unsigned base = step_begin();
+          auto weights = [&](bool whole) __attribute__((always_inline)) {
+            static_for<TILE / 16>([&](auto kbc) {
+              constexpr int kb = decltype(kbc)::value;
+              const f32x4 acc = block_acc(base, kbc);
+              float sc[4];
+              block_scores(acc, t, kb, whole, sc);
+              float w[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) w[e] = __builtin_amdgcn_exp2f(sc[e] - m[e]);
+              const unsigned pw = ps_w + ((4 * kg) * VP + kb * 16 + (lane & 15)) * 2;
+              if constexpr (FAST) {
+                // w * 2^f + 1.5 * 2^23 (exact product, one rounding: RNE) has
+                // the bits of RNE(w * 2^f) + 0x4B400000; NaN -> the constant
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const float y = fmaxf(__builtin_fmaf(w[e], a.fxp_scale, 12582912.0f), 12582912.0f);
+                  den[e] = static_cast<int32_t>(static_cast<uint32_t>(den[e]) + __float_as_uint(y) - 0x4B400000u);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                  const uint32_t pk = p_pack2<DT>(w[e], w[e + 1]);
+                  lds_write_b16(pw + e * VP * 2, pk);
+                  lds_write_b16_hi(pw + (e + 1) * VP * 2, pk);
+                }
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w[e], a.fxp_scale)));
+                  lds_write_b16(pw + e * VP * 2, Io<DT>::store(w[e]));
+                }
+              }
+              __builtin_amdgcn_sched_barrier(0);
+            });
+          };
+          if (FAST && tile_whole(t))
+            weights(true);
+          else
+            weights(false);
+        }
+        {
+          // the wave's P writes complete before its reads (step_begin waits
+          // for its LDS accesses)
+          const unsigned base = step_begin();
+          u32x4 pa[NK0];
+#pragma unroll
+          for (int s = 0; s < NK0; ++s) lds_read_b128(ps_w + ((lane & 15) * VP + s * KI + 8 * kg) * 2, pa[s]);
+#pragma unroll
+          for (int db = 0; db < DBLK; ++db) {
+            uint64_t lo2[NK0], hi2[NK0];
+#pragma unroll
+            for (int s = 0; s < NK0; ++s) {
+              lds_read_b64_tr16(base + voff[db][s][0], lo2[s]);
+              lds_read_b64_tr16(base + voff[db][s][1], hi2[s]);
+            }
+            if constexpr (NK0 == 2) lds_wait_for(pa[0], pa[1], lo2[0], lo2[1]), lds_wait_for(hi2[0], hi2[1]);
+            else lds_wait_for(pa[0], lo2[0], hi2[0]);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NK0; ++s) {
+              const u32x4 vb = {uint32_t(lo2[s]), uint32_t(lo2[s] >> 32), uint32_t(hi2[s]), uint32_t(hi2[s] >> 32)};
+              acc = TR::mma(pa[s], vb, acc);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wv[db][e] = wadd<BITS>(wv[db][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+      // the chunk's denominators over the 16 key lanes, then the fold
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
+        if (mx[e] == -__builtin_inff()) continue;  // no key of the row in this chunk
+        float Mn, fa, fb;
+        merge_factors(Mr[e], mx[e], Mn, fa, fb);
+        Dr[e] = wadd<BITS>(rescale<BITS>(Dr[e], fa), rescale<BITS>(den[e], fb));
+#pragma unroll
+        for (int b = 0; b < DBLK; ++b) Wr[b][e] = wadd<BITS>(rescale<BITS>(Wr[b][e], fa), rescale<BITS>(wv[b][e], fb));
+        Mr[e] = Mn;
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // DMAs into unused stages
+  };
+  if (c_lo < c_hi) {
+    if constexpr (BITS != 64) {
+      if (fast)
+        run(std::true_type{});
+      else
+        run(std::false_type{});
+    } else {
+      run(std::false_type{});
+    }
+  }
+
+  float den_f[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) den_f[e] = fmaxf(acc_f32<BITS>(Dr[e], a.fxp_inv), 1.0e-6f);
+  T* Op = static_cast<T*>(a.o);
+#pragma unroll
+  for (int b = 0; b < DBLK; ++b) {
+    const int d = b * 16 + (lane & 15);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + 4 * kg + e);
+      if (!ri.valid) continue;
+      Op[ri.token * a.so_t + int64_t(ri.head) * a.so_h + d] =
+          Io<DT>::store(div_rn(acc_f32<BITS>(Wr[b][e], a.fxp_inv), den_f[e]));
+    }
+  }
+}
+
 // Fold the per-chunk partials of each (token, head) in ascending chunk order
 // (the kernel's single-pass fold, step for step) and divide.
 template <int DT, int BITS>
@@ -1461,6 +1886,23 @@ int launch_dma(const AttnArgs& a, dim3 grid, hipStream_t st) {
 }
 
 template <int DT, int BITS, int DMAX>
+int launch_prefill_dma(const AttnArgs& a, dim3 grid, hipStream_t st) {
+  if constexpr (DT != FXPR_DTYPE_F32 && (DMAX == 64 || DMAX == 128)) {
+    auto kern = attn_prefill_dma_kernel<DT, BITS, DMAX>;
+    constexpr size_t lds = prefill_dma_lds_bytes<DMAX>();
+    static bool attr_done = false;  // benign race: the attribute is idempotent
+    if (!attr_done) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+      if (e != hipSuccess) return int(e);
+      attr_done = true;
+    }
+    kern<<<grid, kPThreads, lds, st>>>(a);
+  }
+  return 0;
+}
+
+template <int DT, int BITS, int DMAX>
 int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num_tokens, hipStream_t st) {
   dim3 grid(unsigned(num_requests * a.num_kv_heads), unsigned(max_qtiles), unsigned(a.num_splits));
   const bool dma = dma_ok<DT, DMAX>(a);
@@ -1474,7 +1916,13 @@ int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num
         AttnArgs b = a;
         b.pq_rows = kPrefillRows;
         const int ptiles = int(cdiv(int64_t(max_qtiles) * QROWS, PQROWS));
-        attn_prefill_kernel<DT, BITS, DMAX><<<dim3(grid.x, unsigned(ptiles), 1), kPThreads, 0, st>>>(b);
+        const dim3 pgrid(grid.x, unsigned(ptiles), 1);
+        if (dma) {
+          const int e = launch_prefill_dma<DT, BITS, DMAX>(b, pgrid, st);
+          if (e) return e;
+        } else {
+          attn_prefill_kernel<DT, BITS, DMAX><<<pgrid, kPThreads, 0, st>>>(b);
+        }
         if (dma) {
           const int e = launch_dma<DT, BITS, DMAX, false>(b, grid, st);
           if (e) return e;
