@@ -1427,6 +1427,16 @@ template <int DT> __device__ __forceinline__ uint32_t p_pack2(float lo, float hi
   }
 }
 
+// Wait until at most N LDS operations are outstanding (they complete in
+// issue order, so the older ones, whose registers are bound here, are done).
+template <int N, class A, class B> __device__ __forceinline__ void lds_waitn_for(A& a, B& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+template <int N, class A, class B, class C, class D>
+__device__ __forceinline__ void lds_waitn_for(A& a, B& b, C& c, D& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
+
 template <int OFF> __device__ __forceinline__ void lds_read_b128_off(unsigned addr, u32x4& x) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(addr), "n"(OFF) : "memory");
 }
@@ -1565,25 +1575,25 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   // lane%16: chunk 4j + kg (the swizzle depends on the row's low four bits
   // only, so key block kb adds kb * 16 rows). V B-operand reads
   // (ds_read_b64_tr_b16) of d block db: keys s*KI + 8kg + (j>>2) (+4 for the
-  // upper half), columns db*16 + 4*(j&3), j = lane%16.
+  // upper half), columns db*16 + 4*(j&3), j = lane%16: chunk 2 db + b of row
+  // rr sits at slot (2 db + b) ^ swz(rr) = 2 db ^ (b ^ swz(rr)), i.e. at the
+  // d block 0 offset XOR db << 5 (bits 5.. of the chunk part; the row and
+  // half-chunk parts lie outside them).
   unsigned koff[QSTEPS];
 #pragma unroll
   for (int j = 0; j < QSTEPS; ++j) {
     const int rr = lane & 15;
     koff[j] = rr * G::ROWB + (((4 * j + kg) ^ SW::swz(rr)) << 4);
   }
-  unsigned voff[DBLK][NK0][2];
+  unsigned voff0[NK0][2];
 #pragma unroll
-  for (int db = 0; db < DBLK; ++db)
+  for (int s = 0; s < NK0; ++s)
 #pragma unroll
-    for (int s = 0; s < NK0; ++s)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int j = lane & 15;
-        const int rr = s * KI + 8 * kg + (j >> 2) + 4 * h;
-        const int c = 2 * db + ((j & 3) >> 1);
-        voff[db][s][h] = rr * G::ROWB + ((c ^ SW::swz(rr)) << 4) + (j & 1) * 8;
-      }
+    for (int h = 0; h < 2; ++h) {
+      const int j = lane & 15;
+      const int rr = s * KI + 8 * kg + (j >> 2) + 4 * h;
+      voff0[s][h] = rr * G::ROWB + ((((j & 3) >> 1) ^ SW::swz(rr)) << 4) + (j & 1) * 8;
+    }
   const unsigned ps_w = lds0 + PS_OFF + wave * 16 * VP * 2;  // the wave's P [16][VP]
 
   float Mr[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
@@ -1617,20 +1627,38 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       ++step;
       return base;
     };
-    // acc = the MFMA chain of key block kb of the tile at base, as in attn_kernel
-    auto block_acc = [&](unsigned base, auto kbc) __attribute__((always_inline)) -> f32x4 {
-      constexpr int kb = decltype(kbc)::value;
-      u32x4 kf[QSTEPS];
-      static_for<QSTEPS>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        lds_read_b128_off<kb * 16 * G::ROWB>(base + koff[j], kf[j]);
-      });
-      if constexpr (QSTEPS == 4) lds_wait_for(kf[0], kf[1], kf[2], kf[3]);
-      else lds_wait_for(kf[0], kf[1]);
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // The key blocks of the tile at base, software-pipelined: block kb + 1's
+    // fragment reads are issued before block kb's MFMA chain (attn_kernel's
+    // chain per score) and fn(kb, acc); fn may issue LDS writes, which the
+    // next wait covers too (LDS operations complete in order; only the newest
+    // block's QSTEPS reads may remain in flight).
+    auto key_blocks = [&](unsigned base, auto&& fn) __attribute__((always_inline)) {
+      u32x4 kf[2][QSTEPS];
+      auto issue = [&](auto kbc) __attribute__((always_inline)) {
+        constexpr int kb = decltype(kbc)::value;
+        static_for<QSTEPS>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          lds_read_b128_off<kb * 16 * G::ROWB>(base + koff[j], kf[kb & 1][j]);
+        });
+      };
+      issue(std::integral_constant<int, 0>{});
+      static_for<TILE / 16>([&](auto kbc) {
+        constexpr int kb = decltype(kbc)::value;
+        u32x4(&cur)[QSTEPS] = kf[kb & 1];
+        if constexpr (kb + 1 < TILE / 16) {
+          issue(std::integral_constant<int, kb + 1>{});
+          if constexpr (QSTEPS == 4) lds_waitn_for<QSTEPS>(cur[0], cur[1], cur[2], cur[3]);
+          else lds_waitn_for<QSTEPS>(cur[0], cur[1]);
+        } else {
+          if constexpr (QSTEPS == 4) lds_wait_for(cur[0], cur[1], cur[2], cur[3]);
+          else lds_wait_for(cur[0], cur[1]);
+        }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < QSTEPS; ++j) acc = TR::mma(qf[j], kf[j], acc);
-      return acc;
+        for (int j = 0; j < QSTEPS; ++j) acc = TR::mma(qf[j], cur[j], acc);
+        fn(kbc, acc);
+        __builtin_amdgcn_sched_barrier(0);
+      });
     };
     // Scores of key block kb of tile t for the lane's rows (attn_kernel's
     // post-processing); whole: every row of the wave sees the whole tile.
@@ -1661,20 +1689,16 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       for (int t = ta; t < te; ++t) {
         const unsigned base = step_begin();
         if (FAST && tile_whole(t)) {
-          static_for<TILE / 16>([&](auto kbc) {
-            const f32x4 acc = block_acc(base, kbc);
+          key_blocks(base, [&](auto, const f32x4& acc) __attribute__((always_inline)) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) mraw[e] = fmaxf(mraw[e], acc[e]);
-            __builtin_amdgcn_sched_barrier(0);
           });
         } else {
-          static_for<TILE / 16>([&](auto kbc) {
-            const f32x4 acc = block_acc(base, kbc);
+          key_blocks(base, [&](auto kbc, const f32x4& acc) __attribute__((always_inline)) {
             float sc[4];
             block_scores(acc, t, decltype(kbc)::value, false, sc);
 #pragma unroll
             for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], sc[e]);
-            __builtin_amdgcn_sched_barrier(0);
           });
         }
       }
@@ -1697,9 +1721,8 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
         {
           const unsigned base = step_begin();
           auto weights = [&](bool whole) __attribute__((always_inline)) {
-            static_for<TILE / 16>([&](auto kbc) {
+            key_blocks(base, [&](auto kbc, const f32x4& acc) __attribute__((always_inline)) {
               constexpr int kb = decltype(kbc)::value;
-              const f32x4 acc = block_acc(base, kbc);
               float sc[4];
               block_scores(acc, t, kb, whole, sc);
               float w[4];
@@ -1727,7 +1750,6 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
                   lds_write_b16(pw + e * VP * 2, Io<DT>::store(w[e]));
                 }
               }
-              __builtin_amdgcn_sched_barrier(0);
             });
           };
           if (FAST && tile_whole(t))
@@ -1742,26 +1764,43 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
           u32x4 pa[NK0];
 #pragma unroll
           for (int s = 0; s < NK0; ++s) lds_read_b128(ps_w + ((lane & 15) * VP + s * KI + 8 * kg) * 2, pa[s]);
+          // d blocks software-pipelined: block db + 1's V reads go out before
+          // block db's wait (only they may remain in flight)
+          uint64_t vr[2][NK0][2];
+          auto issue_v = [&](auto dbc) __attribute__((always_inline)) {
+            constexpr int db = decltype(dbc)::value;
 #pragma unroll
-          for (int db = 0; db < DBLK; ++db) {
-            uint64_t lo2[NK0], hi2[NK0];
+            for (int s = 0; s < NK0; ++s)
 #pragma unroll
-            for (int s = 0; s < NK0; ++s) {
-              lds_read_b64_tr16(base + voff[db][s][0], lo2[s]);
-              lds_read_b64_tr16(base + voff[db][s][1], hi2[s]);
+              for (int h = 0; h < 2; ++h) lds_read_b64_tr16(base + (voff0[s][h] ^ (db << 5)), vr[db & 1][s][h]);
+          };
+          issue_v(std::integral_constant<int, 0>{});
+          static_for<DBLK>([&](auto dbc) {
+            constexpr int db = decltype(dbc)::value;
+            uint64_t(&cur)[NK0][2] = vr[db & 1];
+            if constexpr (db + 1 < DBLK) {
+              issue_v(std::integral_constant<int, db + 1>{});
+              if constexpr (NK0 == 2) lds_waitn_for<4>(cur[0][0], cur[0][1], cur[1][0], cur[1][1]);
+              else lds_waitn_for<2>(cur[0][0], cur[0][1]);
+            } else {
+              if constexpr (NK0 == 2) lds_wait_for(cur[0][0], cur[0][1], cur[1][0], cur[1][1]);
+              else lds_wait_for(cur[0][0], cur[0][1]);
             }
-            if constexpr (NK0 == 2) lds_wait_for(pa[0], pa[1], lo2[0], lo2[1]), lds_wait_for(hi2[0], hi2[1]);
-            else lds_wait_for(pa[0], lo2[0], hi2[0]);
+            if constexpr (db == 0) {
+              if constexpr (NK0 == 2) lds_wait_for(pa[0], pa[1]);  // already complete: binds the registers
+              else lds_wait_for(pa[0]);
+            }
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NK0; ++s) {
-              const u32x4 vb = {uint32_t(lo2[s]), uint32_t(lo2[s] >> 32), uint32_t(hi2[s]), uint32_t(hi2[s] >> 32)};
+              const u32x4 vb = {uint32_t(cur[s][0]), uint32_t(cur[s][0] >> 32), uint32_t(cur[s][1]),
+                                uint32_t(cur[s][1] >> 32)};
               acc = TR::mma(pa[s], vb, acc);
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) wv[db][e] = wadd<BITS>(wv[db][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
             __builtin_amdgcn_sched_barrier(0);
-          }
+          });
         }
       }
       // the chunk's denominators over the 16 key lanes, then the fold
