@@ -390,22 +390,28 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, 
 // first (integer sums do not depend on the order of tiles). The epilogue
 // stages each wave's C tile through LDS to write whole 16-byte row pieces.
 
-template <int BM_, int BN_, int WGM_, int WGN_, int NS_, int WPE_ = 2> struct BigTile {
+template <int BM_, int BN_, int WGM_, int WGN_, int NSA_, int NSB_, int WPE_ = 2> struct BigTile {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
-  static constexpr int NS = NS_;    // LDS stages (DMAs run NS - 1 stages ahead)
+  // LDS stages of A and of B: each matrix's DMAs run its ring depth - 1
+  // stages ahead (B, the weights streamed from HBM, may get the deeper one)
+  static constexpr int NSA = NSA_, NSB = NSB_;
   static constexpr int WPE = WPE_;  // waves per SIMD the register budget is sized for
   static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
   static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int MB = WM / 16, NB = WN / 16;
 };
-using TB = BigTile<256, 128, 4, 2, 3>;   // one 8-wave workgroup per CU
-using TB2 = BigTile<128, 128, 2, 2, 2>;  // two 4-wave workgroups per CU
+using TB = BigTile<256, 128, 4, 2, 3, 3>;   // one 8-wave workgroup per CU
+// two 4-wave workgroups per CU (80 KB of LDS each)
+#ifndef FXPR_TB2_NSB
+#define FXPR_TB2_NSB 3
+#endif
+using TB2 = BigTile<128, 128, 2, 2, 2, FXPR_TB2_NSB>;
 // int64 accumulators double the integer state (64 x 64 outputs need 128
 // registers of it): one wave per SIMD, one 4-wave workgroup per CU
-using TB64 = BigTile<128, 128, 2, 2, 3, 1>;
+using TB64 = BigTile<128, 128, 2, 2, 3, 3, 1>;
 
 template <class BT> constexpr size_t big_lds_bytes() {
-  constexpr size_t stages = size_t(BT::NS) * (BT::BM + BT::BN) * 128;
+  constexpr size_t stages = (size_t(BT::NSA) * BT::BM + size_t(BT::NSB) * BT::BN) * 128;
   constexpr size_t epi = size_t(BT::WAVES) * BT::WM * (BT::WN + 8) * 2;
   return stages > epi ? stages : epi;
 }
@@ -437,7 +443,9 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
   static_assert(BT::MB == 4 && BT::NB == 4, "fragment asm assumes 64 x 64 wave tiles");
   constexpr int BM = BT::BM, BN = BT::BN, MB = BT::MB, NB = BT::NB, NW = BT::WAVES;
   constexpr int BKS = 64, CH = 8;
-  constexpr int STAGE = (BM + BN) * 128;  // bytes per LDS stage
+  constexpr int NSA = BT::NSA, NSB = BT::NSB;
+  constexpr int A_SLOT = BM * 128, B_SLOT = BN * 128;  // bytes per stage of A, of B
+  constexpr int B_RING = NSA * A_SLOT;                 // the B ring follows the A ring
   constexpr int NIA = BM / 8 / NW;        // A DMA instructions per wave per stage (8 rows each)
   constexpr int NIB = BN / 8 / NW;        // B DMA instructions per wave per stage
   constexpr int NDMA = NIA + NIB;         // vector memory instructions per wave per stage
@@ -482,14 +490,14 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     const int64_t row = isa ? min<int64_t>(m0 + r, args.M - 1) - m0 : min<int64_t>(n0 + r, args.N - 1) - n0;
     voff[q] = uint32_t((row * (isa ? args.lda : args.ldb) + c * CH) * int64_t(sizeof(T)));
   }
-  auto dma = [&](int s, int buf) {  // stage s (64 k from kb0) into LDS buffer buf
+  // stage s (64 k from kb0) of A (isb false) or B into ring slot q % depth
+  auto dma = [&](bool isb, int s, int q) {
     const int soff = s * (BKS * int(sizeof(T)));
+    const unsigned slot = isb ? B_RING + (q % NSB) * B_SLOT : (q % NSA) * A_SLOT;
 #pragma unroll
-    for (int q = 0; q < NDMA; ++q) {
-      const bool isa = q < NIA;
-      const int i = wave + NW * (isa ? q : q - NIA);
-      const unsigned dst = lds0 + buf * STAGE + (isa ? 0 : BM * 128) + i * 1024;
-      buffer_to_lds(isa ? arsrc : brsrc, dst, voff[q], soff);
+    for (int q = isb ? NIA : 0; q < (isb ? NDMA : NIA); ++q) {
+      const int i = wave + NW * (isb ? q - NIA : q);
+      buffer_to_lds(isb ? brsrc : arsrc, lds0 + slot + i * 1024, voff[q], soff);
     }
   };
 
@@ -509,16 +517,18 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
   // f < 4 is A block f, f >= 4 is B block f - 4 (16 rows = 2048 B apart).
   const int kg = lane >> 4, sw = (lane & 15) >> 1;
   const unsigned arow = (wm * BT::WM + (lane & 15)) * 128;
-  const unsigned brow = BM * 128 + (wn * BT::WN + (lane & 15)) * 128;
-  auto frag_addr = [&](int buf, int h, bool isb) -> unsigned {
-    return lds0 + buf * STAGE + ((((h << 2) + kg) ^ sw) << 4) + (isb ? brow : arow);
+  const unsigned brow = (wn * BT::WN + (lane & 15)) * 128;
+  // fragment address in stage s (ring slot s % NSA of A, s % NSB of B)
+  auto frag_addr = [&](int s, int h, bool isb) -> unsigned {
+    const unsigned slot = isb ? B_RING + (s % NSB) * B_SLOT : (s % NSA) * A_SLOT;
+    return lds0 + slot + ((((h << 2) + kg) ^ sw) << 4) + (isb ? brow : arow);
   };
   auto read_frag = [&](unsigned addr, u32x4& x, auto off_tag) {
     constexpr int OFF = decltype(off_tag)::value;
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(x) : "v"(addr), "n"(OFF) : "memory");
   };
-  auto read_frags = [&](int buf, int h, u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
-    const unsigned aa = frag_addr(buf, h, false), bb = frag_addr(buf, h, true);
+  auto read_frags = [&](int st, int h, u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
+    const unsigned aa = frag_addr(st, h, false), bb = frag_addr(st, h, true);
     read_frag(aa, fa[0], std::integral_constant<int, 0>{});
     read_frag(aa, fa[1], std::integral_constant<int, 2048>{});
     read_frag(aa, fa[2], std::integral_constant<int, 4096>{});
@@ -599,11 +609,11 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       for (int j = 0; j < NB; ++j) quantize_block(i, j);
   };
   // Plain (unpipelined) stage, used for the peeled tail tile.
-  auto compute = [&](int buf, bool first) {
+  auto compute = [&](int st, bool first) {
     u32x4 fa[MB], fb[NB];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      read_frags(buf, h, fa, fb);
+      read_frags(st, h, fa, fb);
       lds_wait(fa, fb);
 #pragma unroll
       for (int i = 0; i < MB; ++i)
@@ -636,7 +646,7 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       const T* base = isa ? A + (valid ? row * args.lda + k : 0) : B + (valid ? row * args.ldb + k : 0);
       const uint4 v = load_chunk<false>(base, valid);
       const int rr = isa ? r : r - BM;
-      *reinterpret_cast<uint4*>(smem_raw + st * STAGE + (isa ? 0 : BM * 128) + rr * 128 +
+      *reinterpret_cast<uint4*>(smem_raw + (isa ? st * A_SLOT : B_RING + st * B_SLOT) + rr * 128 +
                                 ((c ^ ((rr >> 1) & 7)) << 4)) = v;
     }
     __syncthreads();
@@ -645,21 +655,33 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     __syncthreads();
   }
 
-  // Pipelined full K-tiles: stage s = 64 k in LDS buffer s % 3, DMAs two
-  // stages ahead. Stages past the end re-load the last one into the free
-  // buffer (never read), so every iteration issues the same DMAs and the
-  // wait count stays exact. Per stage: issue DMAs; the h = 0 MFMAs (with the
-  // previous K-tile's quantisation interleaved at a K-tile start, and the
-  // h = 1 fragment reads issued between them); the h = 1 MFMAs; wait for the
-  // next stage's DMAs and barrier; issue the next stage's h = 0 fragment
-  // reads, which complete while the MFMAs drain.
+  // Pipelined full K-tiles: stage s = 64 k of A in its ring slot s % NSA,
+  // of B in s % NSB; each matrix's DMAs run its depth - 1 stages ahead.
+  // Stages past the end re-load the last one into the free slot (never
+  // read), so every iteration issues the same DMAs and the wait count stays
+  // exact. Per stage: issue the DMAs (the shallower ring's first); the h = 0
+  // MFMAs (with the previous K-tile's quantisation interleaved at a K-tile
+  // start, and the h = 1 fragment reads issued between them); the h = 1
+  // MFMAs; wait for the next stage's DMAs and barrier; issue the next
+  // stage's h = 0 fragment reads, which complete while the MFMAs drain.
   const int nst = 2 * nfull;
   if (nst > 0) {
     u32x4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
-    constexpr int NS = BT::NS;
+    constexpr bool B_DEEP = NSB > NSA;
+    constexpr int NSS = B_DEEP ? NSA : NSB, NSD = B_DEEP ? NSB : NSA;  // shallow, deep depth
+    constexpr int NID = B_DEEP ? NIB : NIA;                             // deep ring's DMAs per stage
+    // DMAs issued after the later of stage s + 1's: the deep ring's of the
+    // same group (if deeper) and NSS - 2 whole groups
+    constexpr int WAITN = NSS == NSD ? NDMA * (NSS - 2) : NID + NDMA * (NSS - 2);
+    // the DMA group of stage j: shallow stage j + NSS - 1, then deep j + NSD - 1
+    // (A counts as the shallow ring when the depths are equal)
+    auto dma_group = [&](int j) {
+      if (j + NSS - 1 >= 0) dma(/*isb=*/!B_DEEP && NSB < NSA, min(j + NSS - 1, nst - 1), j + NSS - 1);
+      if (j + NSD - 1 >= 0) dma(/*isb=*/B_DEEP || NSB == NSA, min(j + NSD - 1, nst - 1), j + NSD - 1);
+    };
 #pragma unroll
-    for (int i = 0; i + 1 < NS; ++i) dma(min(i, nst - 1), i);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA * (NS - 2)) : "memory");
+    for (int j = 1 - NSD; j < 0; ++j) dma_group(j);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
     __builtin_amdgcn_s_barrier();
     read_frags(0, 0, fa0, fb0);
     // tile_start: quantise the previous K-tile's partials block by block.
@@ -668,10 +690,9 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     // to zero, which the rounding constant turns into zero); 64-bit: exactly.
     auto stage = [&](int s, auto tile_start_tag) {
       constexpr bool tile_start = decltype(tile_start_tag)::value;
-      const int buf = s % NS;
-      dma(min(s + NS - 1, nst - 1), (s + NS - 1) % NS);
+      dma_group(s);
       lds_wait(fa0, fb0);
-      const unsigned aa1 = frag_addr(buf, 1, false), bb1 = frag_addr(buf, 1, true);
+      const unsigned aa1 = frag_addr(s, 1, false), bb1 = frag_addr(s, 1, true);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int b = 0; b < MB * NB; ++b) {
@@ -704,11 +725,11 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       __builtin_amdgcn_sched_barrier(0);
       // Own DMAs of stage s + 1 landed (only later stages' may be in
       // flight); the barrier covers everyone's, and everyone's reads of stage
-      // s are done (its buffer is refilled NS - 1 stages later). A plain
+      // s are done (its slots are refilled from the next stage on). A plain
       // s_barrier: __syncthreads() would also fence, i.e. wait for every DMA.
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA * (NS - 2)) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
       __builtin_amdgcn_s_barrier();
-      read_frags((s + 1) % NS, 0, fa0, fb0);
+      read_frags(s + 1, 0, fa0, fb0);
     };
     for (int s = 0; s < nst; s += 2) {
       if constexpr (BITS != 64) {
