@@ -251,6 +251,21 @@ def test_log_softmax_special_rows():
     assert nan_aware_equal(got, want)
 
 
+@pytest.mark.parametrize("b,f", [(32, 16), (16, 8), (16, 16), (32, 32)])
+def test_log_softmax_saturating_sums_and_exact_path(b, f):
+    # rows whose fixed-point denominator saturates (flat rows: every term is
+    # 2^f), next to ordinary rows; (16, 16) and (32, 32) take the exact
+    # per-term path (a term can exceed the rounding constant's range or qmax),
+    # (32, 16) and (16, 8) the rounding-constant one with 32-bit lane sums
+    x = _logits(6, 128_256, seed=b * f)
+    x[0] = 0.0
+    x[1] = -3.5
+    x[2, :64_000] = 7.0
+    got = torch.ops.fxpr.log_softmax_fxp(x.to(DEV), b, f).cpu()
+    want = from_np(R.log_softmax(to_np(x), "bf16", "bf16", b, f), x.dtype)
+    assert nan_aware_equal(got, want), mismatch_report(got, want)
+
+
 def test_log_softmax_close_to_torch():
     x = _logits(16, 32_000, seed=4, dtype=torch.float32)
     got = torch.ops.fxpr.log_softmax_fxp(x.to(DEV), 64, 32).cpu()

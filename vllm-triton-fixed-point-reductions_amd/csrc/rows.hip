@@ -10,6 +10,7 @@
 // in registers between the reduction pass and the output pass so x is read
 // from HBM once.
 
+#include <cmath>
 #include <type_traits>
 
 #include "fxp_device.h"
@@ -291,10 +292,30 @@ int launch_rms(const void* x, void* r, const void* w, void* y, int64_t rows, int
 // (32 x 16 bytes per thread) next to the exp / log temporaries, unspilled.
 constexpr int kLsmThreads = 512;
 
+// quant_nonneg(exp_scaled_to_round(d, f)) by the rounding constant, for
+// 1.4143 * 2^f < 2^22 and <= qmax: the scaled value s = p * 2^(k+f) is exact
+// (p = 2^r for |r| <= 1/2 is in [0.7071, 1.4143], and k + f >= -116, so 2^(k+f)
+// is a normal fp32), fl(s + 1.5 * 2^23) is RNE(s) + 1.5 * 2^23 (the sum lies in
+// [2^23, 2^24), spacing 1; the constant is even), no saturation occurs, and
+// NaN d was raised to the floor as in exp_scaled_to_round. Returns the sum's
+// bit pattern, i.e. the quantised value + 0x4B400000.
+__device__ __forceinline__ uint32_t exp_scaled_rc_bits(float d, int f) {
+  d = fmaxf(d, FXPR_EXP_FLOOR);  // maxNum: NaN -> the floor
+  const float t = __fmul_rn(d, FXPR_LOG2E);
+  const float k = __builtin_rintf(t);
+  const float r = __fsub_rn(t, k);
+  const float s2 = __uint_as_float(static_cast<uint32_t>(static_cast<int>(k) + f + 127) << 23);
+  return __float_as_uint(__builtin_fmaf(exp2_poly(r), s2, 12582912.0f));
+}
+
+// The per-lane sums of the rounding-constant path are plain 32-bit adds: the
+// host enables it only when elements per lane x the largest term stay below
+// 2^32, and one clamp of the exact sum equals the saturating sum of
+// non-negative terms.
 template <int XDT, int YDT, int VEC, int NREG, int BITS>
 __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
     const typename Io<XDT>::T* __restrict__ x, typename Io<YDT>::T* __restrict__ y, int64_t cols,
-    int frac, float inv_scale, uint64_t qmax) {
+    int frac, float inv_scale, uint64_t qmax, int fast_sum) {
   using XT = typename Io<XDT>::T;
   using YT = typename Io<YDT>::T;
   using XV = Vec<XT, VEC>;
@@ -310,6 +331,9 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
   YV* yr = reinterpret_cast<YV*>(y + row * cols);
 
   XV keep[NREG];
+  // IEEE maximum (NaN propagates; gfx950's v_maximum3_f32): the same value
+  // as max_nan up to the sign of a zero maximum, which no output depends on
+  // (x - m and m + ln S come out the same for either zero).
   float m = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < NREG; ++i) {
@@ -317,13 +341,13 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
     if (c < nchunks) {
       keep[i] = xr[c];
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) m = max_nan(m, Io<XDT>::load(keep[i].v[j]));
+      for (int j = 0; j < VEC; ++j) m = __builtin_elementwise_maximum(m, Io<XDT>::load(keep[i].v[j]));
     }
   }
   for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) {
     XV xv = xr[c];
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) m = max_nan(m, Io<XDT>::load(xv.v[j]));
+    for (int j = 0; j < VEC; ++j) m = __builtin_elementwise_maximum(m, Io<XDT>::load(xv.v[j]));
   }
   m = block_max(m, fred);
 
@@ -344,12 +368,28 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
       }
     }
   };
+  if (BITS != 64 && fast_sum) {
+    uint32_t acc32 = 0;
+    auto accum_rc = [&](const XV& xv) {
 #pragma unroll
-  for (int i = 0; i < NREG; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * nthr;
-    if (c < nchunks) accum(keep[i]);
+      for (int j = 0; j < VEC; ++j)
+        acc32 += exp_scaled_rc_bits(__fsub_rn(Io<XDT>::load(xv.v[j]), m), frac) - 0x4B400000u;
+    };
+#pragma unroll
+    for (int i = 0; i < NREG; ++i) {
+      const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+      if (c < nchunks) accum_rc(keep[i]);
+    }
+    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum_rc(xr[c]);
+    acc = static_cast<SumT>(acc32 < qmax ? acc32 : qmax);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NREG; ++i) {
+      const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+      if (c < nchunks) accum(keep[i]);
+    }
+    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum(xr[c]);
   }
-  for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum(xr[c]);
   // The row stays in registers in its storage type: an empty asm "changing"
   // it keeps the compiler from holding every element's fp32 widening (twice
   // the registers) from the sum until the output pass.
@@ -387,15 +427,21 @@ int launch_lsm_vec(const void* x, void* y, int64_t rows, int64_t cols, int bits,
   const int nthr = threads_for(nchunks, NREG, kLsmThreads);
   const float inv = pow2f(-frac);
   const uint64_t qmax = qmax_for_bits(bits);
+  // rounding-constant sums: 1.4143 * 2^f below 2^22 and qmax, and a lane's
+  // terms (each at most 1.4143 * 2^f) summing below 2^32
+  const double term_max = 1.4143 * std::ldexp(1.0, frac) + 1.0;
+  const double lane_elems = double(cdiv(nchunks, nthr)) * VEC;
+  const int fast = bits != 64 && term_max < 4194304.0 && term_max <= double(qmax) &&
+                   lane_elems * term_max < 4294967296.0;
   dim3 grid(static_cast<unsigned>(rows));
   const XT* xp = static_cast<const XT*>(x);
   YT* yp = static_cast<YT*>(y);
   if (bits == 16)
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 16><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 16><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax, fast);
   else if (bits == 32)
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 32><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 32><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax, fast);
   else
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 64><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 64><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax, fast);
   return launch_status();
 }
 
