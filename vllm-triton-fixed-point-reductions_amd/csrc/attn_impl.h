@@ -174,15 +174,6 @@ __device__ __forceinline__ void merge_factors(float M, float mc, float& Mn, floa
   fb = __builtin_amdgcn_exp2f(mc - Mn);
 }
 
-template <int N, class F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-// f(integral_constant<int, i>) for i = 0..N-1, every index a compile-time constant
-template <int N, class F> __device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
-
 template <int DT, int BITS, int DMAX, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
   using TR = Traits<DT>;

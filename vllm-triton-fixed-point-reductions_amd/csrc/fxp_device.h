@@ -10,6 +10,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace fxpr {
 
 // Correctly rounded fp32 square root. HIP's __fsqrt_rn maps to the native
@@ -227,6 +230,15 @@ __device__ __forceinline__ uint64_t wave_sat_sum(uint64_t v, uint64_t qmax) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = sat_add_nonneg(v, __shfl_xor(v, o, 64), qmax);
   return v;
+}
+
+template <int N, class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+// f(integral_constant<int, i>) for i = 0..N-1, every index a compile-time constant
+template <int N, class F> __device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
 }  // namespace fxpr

@@ -426,6 +426,15 @@ constexpr int kBufferDword3 = 0x00020000;
 __device__ __forceinline__ void buffer_to_lds(__amdgpu_buffer_rsrc_t r, unsigned dst, uint32_t voff, int soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)(uintptr_t)dst, 16, voff, soff, 0, 0);
 }
+// Wait until at most N LDS operations are outstanding, tied to the registers
+// the older reads fill (their uses cannot move above it).
+template <int N> __device__ __forceinline__ void lgkm_wait_for(u32x4& a) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait_for(u32x4& a, u32x4& b, u32x4& c, u32x4& d, u32x4& e) {
+  asm volatile("s_waitcnt lgkmcnt(%5)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e) : "n"(N) : "memory");
+}
 // A pointer the caller knows to be wave-uniform, as scalar registers (buffer
 // resources must be).
 template <typename T> __device__ __forceinline__ void* uniform_ptr(const T* p) {
@@ -527,16 +536,18 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     constexpr int OFF = decltype(off_tag)::value;
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(x) : "v"(addr), "n"(OFF) : "memory");
   };
+  // Issue order A0, B0..B3, A1..A3: the stage loop starts on block row 0 as
+  // soon as the first five have landed.
   auto read_frags = [&](int st, int h, u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
     const unsigned aa = frag_addr(st, h, false), bb = frag_addr(st, h, true);
     read_frag(aa, fa[0], std::integral_constant<int, 0>{});
-    read_frag(aa, fa[1], std::integral_constant<int, 2048>{});
-    read_frag(aa, fa[2], std::integral_constant<int, 4096>{});
-    read_frag(aa, fa[3], std::integral_constant<int, 6144>{});
     read_frag(bb, fb[0], std::integral_constant<int, 0>{});
     read_frag(bb, fb[1], std::integral_constant<int, 2048>{});
     read_frag(bb, fb[2], std::integral_constant<int, 4096>{});
     read_frag(bb, fb[3], std::integral_constant<int, 6144>{});
+    read_frag(aa, fa[1], std::integral_constant<int, 2048>{});
+    read_frag(aa, fa[2], std::integral_constant<int, 4096>{});
+    read_frag(aa, fa[3], std::integral_constant<int, 6144>{});
   };
   auto lds_wait = [&](u32x4 (&fa)[MB], u32x4 (&fb)[NB]) {
     asm volatile("s_waitcnt lgkmcnt(0)"
@@ -684,6 +695,10 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
     __builtin_amdgcn_s_barrier();
     read_frags(0, 0, fa0, fb0);
+    // Landed before the loop: the compiler may move the loop's fragment
+    // registers into place here, and an inline-asm read's output looks ready
+    // to it at issue.
+    lds_wait(fa0, fb0);
     // tile_start: quantise the previous K-tile's partials block by block.
     // 16- and 32-bit accumulators: by the rounding constant (a K-tile that
     // fails tile_fast was quantised exactly beforehand and its partials set
@@ -691,32 +706,51 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     auto stage = [&](int s, auto tile_start_tag) {
       constexpr bool tile_start = decltype(tile_start_tag)::value;
       dma_group(s);
-      lds_wait(fa0, fb0);
       const unsigned aa1 = frag_addr(s, 1, false), bb1 = frag_addr(s, 1, true);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int b = 0; b < MB * NB; ++b) {
-        const int i = b / NB, j = b % NB;
+      // Block row i: its quantisation (at a K-tile start; registers only, so
+      // it runs while the row's fragments land), a wait for them (LDS
+      // operations complete in issue order: A(i+1..3) and the h = 1 reads
+      // issued so far, two per row, may still be in flight), its MFMAs with
+      // the h = 1 reads in between.
+      auto row_prologue = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;
         if constexpr (tile_start) {
-          if constexpr (BITS == 64)
-            quantize_block(i, j);
-          else
-            quantize_block_fast(i, j);
+#pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            if constexpr (BITS == 64)
+              quantize_block(i, j);
+            else
+              quantize_block_fast(i, j);
+          }
         }
+        if constexpr (BITS == 64) {
+          // int64 accumulators spill into AGPRs: the compiler may copy a
+          // fragment register it takes for ready, so all of them are bound
+          // to one full wait before their first use
+          if constexpr (i == 0) lds_wait(fa0, fb0);
+        } else if constexpr (i == 0) {
+          lgkm_wait_for<3>(fa0[0], fb0[0], fb0[1], fb0[2], fb0[3]);
+        } else {
+          lgkm_wait_for<3 + i>(fa0[i]);
+        }
+      };
+      // compile-time block index: every read and wait at a fixed place (a
+      // runtime switch would put the reads on branches, where the compiler
+      // may copy registers whose loads are still in flight)
+      static_for<MB * NB>([&](auto bc) {
+        constexpr int b = decltype(bc)::value, i = b / NB, j = b % NB;
+        if constexpr (j == 0) row_prologue(std::integral_constant<int, i>{});
         mma(i, j, fa0[i], fb0[j], tile_start);
-        switch (b) {
-          case 0: read_frag(aa1, fa1[0], std::integral_constant<int, 0>{}); break;
-          case 2: read_frag(aa1, fa1[1], std::integral_constant<int, 2048>{}); break;
-          case 4: read_frag(aa1, fa1[2], std::integral_constant<int, 4096>{}); break;
-          case 6: read_frag(aa1, fa1[3], std::integral_constant<int, 6144>{}); break;
-          case 8: read_frag(bb1, fb1[0], std::integral_constant<int, 0>{}); break;
-          case 10: read_frag(bb1, fb1[1], std::integral_constant<int, 2048>{}); break;
-          case 12: read_frag(bb1, fb1[2], std::integral_constant<int, 4096>{}); break;
-          case 14: read_frag(bb1, fb1[3], std::integral_constant<int, 6144>{}); break;
-          default: break;
+        if constexpr (b % 2 == 0) {
+          constexpr int f = b / 2;  // h = 1 fragment f: A 0..3, then B 0..3
+          if constexpr (f < MB)
+            read_frag(aa1, fa1[f], std::integral_constant<int, 2048 * f>{});
+          else
+            read_frag(bb1, fb1[f - MB], std::integral_constant<int, 2048 * (f - MB)>{});
         }
         __builtin_amdgcn_sched_barrier(0);
-      }
+      });
       lds_wait(fa1, fb1);
 #pragma unroll
       for (int i = 0; i < MB; ++i)
