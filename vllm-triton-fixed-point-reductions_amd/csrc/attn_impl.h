@@ -1531,7 +1531,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   if (c_lo < c_hi) {
     dent = page_entry(cur_tile());
 #pragma unroll
-    for (int i = 0; i + 1 < NS; ++i) {
+    for (int i = 0; i + 2 < NS; ++i) {
       dma_tile(cur_isv(), cur_tile(), dent, i);
       advance();
       dent = page_entry(cur_tile());
@@ -1605,19 +1605,29 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   const bool fast = fast_den && !(a.softcap_log2 > 0.0f) && !a.alibi && a.scale_log2 > 0.0f;
   auto run = [&](auto fast_tag) __attribute__((always_inline)) {
     constexpr bool FAST = decltype(fast_tag)::value;
-    int step = 0;
-    auto step_begin = [&]() -> unsigned {
-      // own DMAs of this step landed (only later steps' in flight), own LDS
-      // accesses done; the barrier makes both everyone's
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(G::NDMA * (NS - 2)) : "memory");
+    // A step consumes C ring entries (1: a K tile of phase 0; 2: a tile's K
+    // and V in phase 1) and issues C more: the cursor stays NS - 2 entries
+    // ahead, so the two slots a 2-entry step refills are free. Returns the
+    // step's first entry (stage entry % NS).
+    int step = 0;  // entries consumed
+    auto step_begin = [&](auto c_tag) -> int {
+      constexpr int C = decltype(c_tag)::value;
+      // own DMAs of this step's entries landed (only the NS - 2 - C later
+      // entries' in flight), own LDS accesses done; the barrier makes both
+      // everyone's
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(G::NDMA * (NS - 2 - C)) : "memory");
       __builtin_amdgcn_s_barrier();
-      dma_tile(cur_isv(), cur_tile(), dent, (step + NS - 1) % NS);
-      advance();
-      dent = page_entry(cur_tile());
-      const unsigned base = lds0 + (step % NS) * G::TILEB;
-      ++step;
-      return base;
+#pragma unroll
+      for (int u = 0; u < C; ++u) {
+        dma_tile(cur_isv(), cur_tile(), dent, (step + NS - 2 + u) % NS);
+        advance();
+        dent = page_entry(cur_tile());
+      }
+      const int e = step;
+      step += C;
+      return e;
     };
+    auto stage_base = [&](int e) -> unsigned { return lds0 + (e % NS) * G::TILEB; };
     // The key blocks of the tile at base, software-pipelined: block kb + 1's
     // fragment reads are issued before block kb's MFMA chain (attn_kernel's
     // chain per score) and fn(kb, acc); fn may issue LDS writes, which the
@@ -1678,7 +1688,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       float mraw[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
       // phase 0: the chunk's row maxima
       for (int t = ta; t < te; ++t) {
-        const unsigned base = step_begin();
+        const unsigned base = stage_base(step_begin(std::integral_constant<int, 1>{}));
         if (FAST && tile_whole(t)) {
           key_blocks(base, [&](auto, const f32x4& acc) __attribute__((always_inline)) {
 #pragma unroll
@@ -1709,8 +1719,9 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
 #pragma unroll
         for (int e = 0; e < 4; ++e) wv[b][e] = 0;
       for (int t = ta; t < te; ++t) {
+        const int e = step_begin(std::integral_constant<int, 2>{});  // K(t), then V(t)
         {
-          const unsigned base = step_begin();
+          const unsigned base = stage_base(e);
           auto weights = [&](bool whole) __attribute__((always_inline)) {
             key_blocks(base, [&](auto kbc, const f32x4& acc) __attribute__((always_inline)) {
               constexpr int kb = decltype(kbc)::value;
@@ -1749,9 +1760,9 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
             weights(false);
         }
         {
-          // the wave's P writes complete before its reads (step_begin waits
-          // for its LDS accesses)
-          const unsigned base = step_begin();
+          // the wave's own P writes complete before its reads
+          lds_wait();
+          const unsigned base = stage_base(e + 1);
           u32x4 pa[NK0];
 #pragma unroll
           for (int s = 0; s < NK0; ++s) lds_read_b128(ps_w + ((lane & 15) * VP + s * KI + 8 * kg) * 2, pa[s]);
