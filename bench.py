@@ -216,7 +216,9 @@ def wl_gemm(steps, warmup, M, N=128256, K=4096, dtype_name="bf16", int_bits=32, 
 
 def wl_decode(steps, warmup, splits=0, int_bits=32, frac_bits=16, B=64, hq=32, hkv=8, d=128, ps=16,
               pool=1 << 16, seed=0):
-    """Paged split-K decode attention. Context lengths,
+    """Paged split-K decode attention: 64 one-token requests, contexts
+    U[512, 8192], 16-token pages in a 2^16-page pool (BASELINE.json's fourth
+    configuration). Context lengths,
     the block table (consecutive slices of a permutation of the pool) and q
     come from a seeded CPU generator; the 4 GiB KV pool from a seeded device
     generator (generating it on the host would dominate the run)."""
