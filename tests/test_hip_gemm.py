@@ -199,6 +199,24 @@ def test_gemm_big_nonfinite_partials(dtype, M):
     assert torch.equal(got, want), mismatch_report(got, want)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", _BIG_M)
+def test_gemm_big_split_k_invariance(dtype, M):
+    # the large-M kernel's split-K instantiation: each split's K-tiles (with a
+    # partial last tile in the last split) through the same rounding-constant
+    # path, partial sums in the workspace, then the reduce; every split count
+    # gives the unsplit bits, which equal the oracle on exact dots
+    g = torch.Generator("cpu").manual_seed(17 + M)
+    K, N = 1000, 384
+    a = _dyadic((M, K), -3, 3, -5, g, dtype)
+    b = _dyadic((K, N), -3, 3, 0, g, dtype)
+    a[M // 2:M // 2 + 16, 256:384] *= 512  # one K-tile of some rows on the exact path
+    want = _oracle(a, b, None, 32, 16)
+    for s in (1, 2, 3, 5, 8):  # 5: the last split has no K-tiles
+        got = _run(a, b, bits=32, frac=16, split_k=s, b_layout="nk")
+        assert torch.equal(got, want), (s, mismatch_report(got, want))
+
+
 # --- restated reference tests (fxpr_vllm/_tests/test_gemm.py) ---------------
 
 @pytest.mark.parametrize("M,N,K", [(4, 4, 16), (3, 7, 16), (1, 1, 32), (8, 16, 32)])

@@ -752,11 +752,17 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
         __builtin_amdgcn_sched_barrier(0);
       });
       lds_wait(fa1, fb1);
+      // With two 4-wave workgroups per CU, two waves share each SIMD: the
+      // one in this MFMA burst takes issue priority, so the other's VALU and
+      // LDS instructions go in the gaps between its MFMAs rather than ahead
+      // of them (1-4 % at M = 8192).
+      if constexpr (NW == 4 && BT::WPE == 2) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j) mma(i, j, fa1[i], fb1[j], false);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NW == 4 && BT::WPE == 2) __builtin_amdgcn_s_setprio(0);
       // Own DMAs of stage s + 1 landed (only later stages' may be in
       // flight); the barrier covers everyone's, and everyone's reads of stage
       // s are done (its slots are refilled from the next stage on). A plain
