@@ -388,6 +388,24 @@ def test_prefill_score_variants_match_split_path(bits, frac, window, sign):
     assert torch.equal(one.view(torch.int16), split.view(torch.int16))
 
 
+@pytest.mark.parametrize("bits,frac", [(16, 8), (32, 16)])
+def test_prefill_weighted_v_paths_match_split_path(bits, frac):
+    # the fast prefill variant quantises a d block of weighted V by the
+    # rounding constant when every partial is in range, else exactly: V dims
+    # 32..47 of kv head 0 scaled by 2^12 push that block out of range (16-bit
+    # sums saturate), the other blocks stay fast, and a NaN value sends its
+    # block to the exact path; bits equal the split path's
+    dtype = torch.bfloat16
+    q, kv, qsl, sl, bt = _prefix_case([300, 180], [700, 90], 8, 2, 128, 16, dtype, seed=bits + 7)
+    kv[:, 1, :, 0, 32:48] *= 4096
+    kv[bt[1, 2].long(), 1, 5, 1, 70] = float("nan")  # V of key 37 of request 1, kv head 1
+    kw = dict(scale=1 / math.sqrt(128), bits=bits, frac=frac)
+    one = attend(q, kv, qsl, sl, bt, 300, 1, **kw)
+    split = attend(q, kv, qsl, sl, bt, 300, 4, **kw)
+    assert torch.equal(one.view(torch.int16), split.view(torch.int16))
+    assert torch.isfinite(one[:300].float()).all()  # request 0 holds no NaN
+
+
 def test_prefill_rows_equal_their_decode_step():
     # the last prompt token computed inside a 400-token prefill equals the
     # same token computed as a one-token decode over the cached prefix

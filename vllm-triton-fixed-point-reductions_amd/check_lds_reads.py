@@ -20,6 +20,15 @@ to its wait; a read whose destination is copied on a branch edge (the way a
 compiler moves registers into place for a join) appears as such a copy on the
 fall-through side as well.
 
+A second scan covers every kernel of the sources: an inline-asm instruction
+that reads the result of an MFMA. The compiler inserts the wait states an
+MFMA result needs before its own instructions read it, but not before an asm
+statement, so along every path of the control-flow graph (fall-through and
+branch edges) from an MFMA writing a register to an asm instruction reading
+it, at least MFMA_WAIT_STATES wait states must pass (one per instruction,
+N + 1 per s_nop N): the most any MFMA needs on gfx950 (16-pass shapes), more
+than the 8 the compiler itself keeps for a 16x16x32 result.
+
 Exit status 1 if any such use is found.
 """
 
@@ -38,6 +47,8 @@ from build import COMMON_FLAGS, CSRC, hipcc  # noqa: E402
 
 DEFAULT_SOURCES = ["gemm_bf16.hip", "gemm_f16.hip", "attn_bf16.hip", "attn_f16.hip"]
 KERNELS = re.compile(r"^(_ZN4fxpr\w*(gemm_big_kernel|attn_dma_kernel|attn_prefill_dma_kernel)\w*):")
+ALL_KERNELS = re.compile(r"^(_ZN4fxpr\w+):")
+MFMA_WAIT_STATES = 19
 
 
 def _vregs(tok: str) -> set[int]:
@@ -80,6 +91,98 @@ def scan_kernel(lines: list[str]) -> list[str]:
     return found
 
 
+def _blocks(lines: list[str]) -> tuple[list[list[tuple[str, bool]]], list[list[int]]]:
+    """Basic blocks of one kernel's text (instruction, inside inline asm) and
+    each block's predecessors."""
+    blocks: list[list[tuple[str, bool]]] = [[]]
+    names: dict[str, int] = {}
+    in_asm = False
+    for text in lines:
+        t = text.strip()
+        if t == ";;#ASMSTART":
+            in_asm = True
+            continue
+        if t == ";;#ASMEND":
+            in_asm = False
+            continue
+        m = re.match(r"^(\.LBB\w+):", t)
+        if m:
+            if blocks[-1]:
+                blocks.append([])
+            names[m.group(1)] = len(blocks) - 1
+            continue
+        if not t or t[0] in ";.":
+            continue
+        blocks[-1].append((t, in_asm))
+        if t.split()[0].startswith(("s_branch", "s_cbranch", "s_endpgm", "s_setpc")):
+            blocks.append([])
+    preds: list[list[int]] = [[] for _ in blocks]
+    for b, ins in enumerate(blocks):
+        last = ins[-1][0].split() if ins else [""]
+        if last[0].startswith(("s_branch", "s_cbranch")) and last[-1] in names:
+            preds[names[last[-1]]].append(b)
+        if b + 1 < len(blocks) and not last[0].startswith(("s_branch", "s_endpgm", "s_setpc")):
+            preds[b + 1].append(b)
+    return blocks, preds
+
+
+def _wait_states(t: str) -> int:
+    op = t.split()
+    return int(op[1], 0) + 1 if op[0] == "s_nop" else 1
+
+
+def scan_mfma_reads(lines: list[str], need: int = MFMA_WAIT_STATES) -> list[str]:
+    """Inline-asm instructions naming an MFMA's destination registers fewer
+    than `need` wait states after it on some path."""
+    blocks, preds = _blocks(lines)
+    found = []
+    for b, ins in enumerate(blocks):
+        for k, (t, in_asm) in enumerate(ins):
+            if not in_asm:
+                continue
+            # every register the instruction names: a read of an MFMA result
+            # too early sees the old value, a write (a load's destination)
+            # too early can be overwritten by the MFMA's late write-back
+            regs0: set[str] = set()
+            for part in t.partition(" ")[2].replace(",", " ").split():
+                regs0 |= _vregs(part)
+            if not regs0:
+                continue
+            # backward search over (block, registers still traced). A
+            # compiler-generated instruction naming a register ends its trace:
+            # the compiler kept the MFMA's wait states before it, so the write
+            # had landed by then.
+            best: dict[tuple[int, frozenset], int] = {}
+            work = [(b, k, 0, frozenset(regs0))]
+            hit = None
+            while work and hit is None:
+                blk, pos, dist, regs = work.pop()
+                for j in range(pos - 1, -1, -1):
+                    u, u_asm = blocks[blk][j]
+                    uop, _, urest = u.partition(" ")
+                    if uop.startswith("v_mfma") and _vregs(urest.split(",")[0].strip()) & regs:
+                        hit = (dist, u)
+                        break
+                    if not u_asm:
+                        named: set[str] = set()
+                        for part in urest.replace(",", " ").split():
+                            named |= _vregs(part)
+                        regs = regs - named
+                        if not regs:
+                            break
+                    dist += _wait_states(u)
+                    if dist >= need:
+                        break
+                else:
+                    for p in preds[blk]:
+                        if dist < best.get((p, regs), need):
+                            best[(p, regs)] = dist
+                            work.append((p, len(blocks[p]), dist, regs))
+            if hit is not None:
+                found.append(f"{t}  ({hit[0]} wait states after {hit[1]})")
+    return found
+
+
 def check_asm(path: Path) -> dict[str, list[str]]:
     src = path.read_text().splitlines()
     out: dict[str, list[str]] = {}
@@ -90,9 +193,28 @@ def check_asm(path: Path) -> dict[str, list[str]]:
             i += 1
             continue
         j = i + 1
-        while j < len(src) and "s_endpgm" not in src[j]:
+        # to the function's end: blocks placed after an s_endpgm (an early
+        # exit, or code the compiler lays out past the return) are scanned too
+        while j < len(src) and not src[j].startswith(".Lfunc_end"):
             j += 1
         out[m.group(1)] = scan_kernel(src[i + 1:j])
+        i = j
+    return out
+
+
+def check_mfma_asm(path: Path) -> dict[str, list[str]]:
+    src = path.read_text().splitlines()
+    out: dict[str, list[str]] = {}
+    i = 0
+    while i < len(src):
+        m = ALL_KERNELS.match(src[i])
+        if not m:
+            i += 1
+            continue
+        j = i + 1
+        while j < len(src) and not src[j].startswith(".Lfunc_end"):
+            j += 1
+        out[m.group(1)] = scan_mfma_reads(src[i + 1:j])
         i = j
     return out
 
@@ -109,7 +231,7 @@ def compile_asm(source: Path, out_dir: Path) -> Path:
 
 def main(argv: list[str]) -> int:
     sources = [CSRC / s for s in (argv or DEFAULT_SOURCES)]
-    bad = 0
+    bad = bad_mfma = 0
     with tempfile.TemporaryDirectory() as tmp, cf.ThreadPoolExecutor(max_workers=4) as ex:
         for asm in ex.map(lambda s: compile_asm(s, Path(tmp)), sources):
             for kernel, hits in check_asm(asm).items():
@@ -118,8 +240,15 @@ def main(argv: list[str]) -> int:
                     print(f"{asm.stem}: {kernel}")
                     for h in hits[:8]:
                         print("   ", h)
+            for kernel, hits in check_mfma_asm(asm).items():
+                if hits:
+                    bad_mfma += len(hits)
+                    print(f"{asm.stem}: {kernel} (MFMA result read by inline asm)")
+                    for h in hits[:8]:
+                        print("   ", h)
     print("LDS read check:", "ok" if bad == 0 else f"{bad} early uses")
-    return 1 if bad else 0
+    print("MFMA result check:", "ok" if bad_mfma == 0 else f"{bad_mfma} asm reads too close")
+    return 1 if bad or bad_mfma else 0
 
 
 if __name__ == "__main__":
