@@ -669,6 +669,10 @@ __device__ __forceinline__ void lds_wait_for(A& a, B& b, C& c, D& d) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : : "memory");
 }
 
+// Cache-policy operand of the buffer/global load builtins on gfx950: bit 1
+// is nt (non-temporal; glc/sc0 is bit 0, sc1 bit 4).
+constexpr int kCpolNT = 2;
+
 template <int DT, int BITS, int DMAX, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   static_assert(DT != FXPR_DTYPE_F32, "16-bit inputs only");
@@ -742,7 +746,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
                            uint64_t(uint32_t(g)) * uint32_t(sh) + uint32_t(c * 8);
       const T* src = (isv ? Vc : Kc) + off;
       const unsigned dst = lds0 + buf * G::TILEB + row0q * G::ROWB;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
+      // non-temporal (cache-policy bit nt): every K and V row is read once
+      // per launch (4.30 -> 4.70 TB/s on the decode batch)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, kCpolNT);
     }
   };
 
@@ -1499,6 +1505,8 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
                            uint64_t(uint32_t(g)) * uint32_t(sh) + uint32_t(c * 8);
       const T* src = (isv ? Vc : Kc) + off;
       const unsigned dst = lds0 + buf * G::TILEB + row0q * G::ROWB;
+      // (temporal: a workgroup reads each K tile twice and neighbouring
+      // row blocks share tiles through L2; nt measured 5 % slower)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
     }
   };

@@ -146,6 +146,23 @@ int launch_row_sum(const void* q, void* out, int obits, int64_t rows, int64_t co
 // rrms = 1 / sqrt(fl32(T) * 2^-f / H + eps).
 // Pass 2: u = fl32(IO(v)) (what was stored) or fl32(x); y = IO((u * w) * rrms).
 
+// Streamed rows are read and written once: non-temporal 16-byte accesses
+// (global_load/store ... nt) keep them from displacing reused lines in the
+// caches (RMSNorm [16384, 4096] + residual: 5.80 -> 6.05 TB/s).
+typedef unsigned nt_u32x4 __attribute__((ext_vector_type(4)));
+template <class V> __device__ __forceinline__ V nt_load(const V* p) {
+  if constexpr (sizeof(V) == 16)
+    return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4*>(p)));
+  else
+    return *p;
+}
+template <class V> __device__ __forceinline__ void nt_store(V* p, const V& v) {
+  if constexpr (sizeof(V) == 16)
+    __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x4, v), reinterpret_cast<nt_u32x4*>(p));
+  else
+    *p = v;
+}
+
 template <int DT, int VEC, int NREG, int BITS, bool RES>
 __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
     const typename Io<DT>::T* __restrict__ x, typename Io<DT>::T* __restrict__ r,
@@ -168,12 +185,12 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
   uint64_t acc = 0;
 
   auto pass1 = [&](int64_t c, float (&u)[VEC]) {
-    V xv = xr[c];
+    V xv = nt_load(xr + c);
     float v[VEC];
 #pragma unroll
     for (int j = 0; j < VEC; ++j) v[j] = Io<DT>::load(xv.v[j]);
     if constexpr (RES) {
-      V rv = rr[c];
+      V rv = nt_load(rr + c);
       V sv;
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
@@ -181,7 +198,7 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
         sv.v[j] = Io<DT>::store(v[j]);
         u[j] = Io<DT>::load(sv.v[j]);
       }
-      rr[c] = sv;
+      nt_store(rr + c, sv);
     } else {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) u[j] = v[j];
@@ -212,7 +229,7 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
 #pragma unroll
     for (int j = 0; j < VEC; ++j)
       yv.v[j] = Io<DT>::store(__fmul_rn(__fmul_rn(u[j], Io<DT>::load(wv.v[j])), rrms));
-    yr[c] = yv;
+    nt_store(yr + c, yv);
   };
 
 #pragma unroll
