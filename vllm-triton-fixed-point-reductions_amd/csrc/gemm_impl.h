@@ -846,7 +846,8 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
         const u32x4 v = *reinterpret_cast<const u32x4*>(ep + row * EP + col);
         if (m < args.M) {
           if (n + CH <= args.N) {
-            *reinterpret_cast<u32x4*>(C + m * args.scm + n) = v;
+            // C is written once: non-temporal (0-3 %, most at M = 256)
+            __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + m * args.scm + n));
           } else {
             const T* e = reinterpret_cast<const T*>(&v);
             for (int q = 0; q < CH; ++q)
