@@ -142,7 +142,7 @@ def _dyadic(shape, lo, hi, exp2, g, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M", _BIG_M)
-@pytest.mark.parametrize("bits,frac", [(32, 16), (16, 8), (32, 8), (16, 12)])
+@pytest.mark.parametrize("bits,frac", [(32, 16), (16, 8), (32, 8), (16, 12), (64, 16)])
 @pytest.mark.parametrize("K", [384, 300])
 def test_gemm_big_rounding_constant_ties(dtype, M, bits, frac, K):
     # products are multiples of 2^-(f+1): many partials lie exactly halfway
@@ -170,8 +170,8 @@ def test_gemm_big_mixed_tile_paths(dtype, M):
     a[64:128, 128:256] *= 256  # one wave row, second K-tile
     a[M - 64:M - 48, 384:512] *= 256  # 16 rows of one wave, last K-tile
     a[3, 0:128] *= 256  # a single row, first K-tile
-    for bits in (32, 16):
-        frac = 16 if bits == 32 else 8
+    for bits in (32, 16, 64):
+        frac = 8 if bits == 16 else 16
         got = _run(a, b, bits=bits, frac=frac, b_layout="nk")
         want = _oracle(a, b, None, bits, frac)
         assert torch.equal(got, want), (bits, mismatch_report(got, want))
@@ -194,9 +194,10 @@ def test_gemm_big_nonfinite_partials(dtype, M):
     if dtype == torch.bfloat16:
         a[200, 140] = 2.0 ** 100  # finite inputs whose products overflow fp32
         b[140, :] = b[140, :] * 2.0 ** 30
-    got = _run(a, b, bits=32, frac=16, b_layout="nk")
-    want = _oracle(a, b, None, 32, 16)
-    assert torch.equal(got, want), mismatch_report(got, want)
+    for bits in (32, 64):
+        got = _run(a, b, bits=bits, frac=16, b_layout="nk")
+        want = _oracle(a, b, None, bits, 16)
+        assert torch.equal(got, want), (bits, mismatch_report(got, want))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -64,8 +64,9 @@ extern "C" int fxpr_gemm(const void* a, const void* b, const float* bias, void* 
   args.scn = stride_cn;
   args.scale = pow2f(frac_bits);
   args.inv_scale = pow2f(-frac_bits);
-  args.fast_lim = (int_bits == 64 || frac_bits < 0) ? 0.0f
-                                                    : (int_bits == 16 ? 32767.0f : 4194304.0f) * pow2f(-frac_bits);
+  // the large-M kernel's rounding-constant bound on a K-tile's partials:
+  // |P * 2^f| below 2^22 (and 32767 for 16-bit sums)
+  args.fast_lim = frac_bits < 0 ? 0.0f : (int_bits == 16 ? 32767.0f : 4194304.0f) * pow2f(-frac_bits);
   args.ktiles = int(cdiv(k, ktile_for(io_dtype)));
   args.tiles_per_split = int(cdiv(args.ktiles, splits));
   args.c_vec = (stride_cn == 1 || n == 1) && stride_cm % ch == 0 && aligned(c, 16);

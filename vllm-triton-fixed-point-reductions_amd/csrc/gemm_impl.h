@@ -581,27 +581,31 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
   // |P| < fast_lim (so |P * 2^f| < 2^22, exact): fl32(x + 1.5 * 2^23) is
   // RNE(x) + 1.5 * 2^23 (the sum lies in [2^23, 2^24), where the spacing is
   // 1, and the constant is even, so a tie goes to the same even integer), and
-  // its bit pattern minus the constant's is RNE(x). No saturation can occur.
-  // Same bits as quantize_block; two instructions per element instead of four.
+  // its bit pattern minus the constant's is RNE(x). No saturation can occur
+  // (and for 64-bit sums RNE(x) fits 32 bits, sign-extended into the add).
+  // Same bits as quantize_block; two instructions per element instead of four
+  // (64-bit: five instead of about eight).
   // (The accumulator update is written as an instruction: from C the
   // compiler splits the add off into extra moves and adds.)
   const float magic = 12582912.0f;  // 1.5 * 2^23, bit pattern 0x4B400000
   const uint32_t neg_magic_bits = 0xB4C00000u;  // -0x4B400000 mod 2^32
   auto quantize_block_fast = [&](int i, int j) {
-    if constexpr (BITS != 64) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float y = __builtin_fmaf(P[i][j][r], args.scale, magic);
+    for (int r = 0; r < 4; ++r) {
+      const float y = __builtin_fmaf(P[i][j][r], args.scale, magic);
+      if constexpr (BITS == 64) {
+        // the 32-bit RNE(x), sign-extended into the 64-bit sum
+        const int32_t q = static_cast<int32_t>(__float_as_uint(y) + neg_magic_bits);
+        I[i][j][r] = wrap_add<BITS>(I[i][j][r], q);
+      } else {
         asm("v_add3_u32 %0, %0, %1, %2" : "+v"(I[i][j][r]) : "v"(y), "v"(neg_magic_bits));
       }
     }
   };
   // Whether every partial of the wave's tile satisfies |P| < fast_lim (NaN
   // and infinities fail: v_maximum3_f32 propagates NaN).
-  auto tile_fast = [&]() -> bool {
-    if constexpr (BITS == 64) {
-      return false;
-    } else {
+  auto tile_fast = [&]() __attribute__((always_inline)) -> bool {
+    {
       float m[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < MB; ++i)
@@ -618,7 +622,7 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       return __builtin_amdgcn_ballot_w64(!(mm < args.fast_lim)) == 0;
     }
   };
-  auto quantize = [&]() {
+  auto quantize = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -704,10 +708,10 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     // registers into place here, and an inline-asm read's output looks ready
     // to it at issue.
     lds_wait(fa0, fb0);
-    // tile_start: quantise the previous K-tile's partials block by block.
-    // 16- and 32-bit accumulators: by the rounding constant (a K-tile that
-    // fails tile_fast was quantised exactly beforehand and its partials set
-    // to zero, which the rounding constant turns into zero); 64-bit: exactly.
+    // tile_start: quantise the previous K-tile's partials block by block by
+    // the rounding constant (a K-tile that fails tile_fast was quantised
+    // exactly beforehand and its partials set to zero, which the rounding
+    // constant turns into zero).
     auto stage = [&](int s, auto tile_start_tag) {
       constexpr bool tile_start = decltype(tile_start_tag)::value;
       dma_group(s);
@@ -722,12 +726,7 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
         constexpr int i = decltype(ic)::value;
         if constexpr (tile_start) {
 #pragma unroll
-          for (int j = 0; j < NB; ++j) {
-            if constexpr (BITS == 64)
-              quantize_block(i, j);
-            else
-              quantize_block_fast(i, j);
-          }
+          for (int j = 0; j < NB; ++j) quantize_block_fast(i, j);
         }
         if constexpr (BITS == 64) {
           // int64 accumulators spill into AGPRs: the compiler may copy a
@@ -777,14 +776,12 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       read_frags(s + 1, 0, fa0, fb0);
     };
     for (int s = 0; s < nst; s += 2) {
-      if constexpr (BITS != 64) {
-        if (!tile_fast()) {  // rare: partials out of the fast range, NaN or infinite
-          quantize();
+      if (!tile_fast()) {  // rare: partials out of the fast range, NaN or infinite
+        quantize();
 #pragma unroll
-          for (int i = 0; i < MB; ++i)
+        for (int i = 0; i < MB; ++i)
 #pragma unroll
-            for (int j = 0; j < NB; ++j) P[i][j] = zero4;
-        }
+          for (int j = 0; j < NB; ++j) P[i][j] = zero4;
       }
       stage(s, std::true_type{});
       stage(s + 1, std::false_type{});
