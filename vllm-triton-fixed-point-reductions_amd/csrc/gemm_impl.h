@@ -412,8 +412,9 @@ using TB = BigTile<256, 128, 4, 2, 3, 3>;   // one 8-wave workgroup per CU
 #endif
 using TB2 = BigTile<128, 128, 2, 2, 2, FXPR_TB2_NSB>;
 // int64 accumulators double the integer state (64 x 64 outputs need 128
-// registers of it): one wave per SIMD, one 4-wave workgroup per CU
-using TB64 = BigTile<128, 128, 2, 2, 3, 3, 1>;
+// registers of it): one wave per SIMD, one 4-wave workgroup per CU; A two
+// stages deep, B three (2 % over three of each)
+using TB64 = BigTile<128, 128, 2, 2, 2, 3, 1>;
 
 template <class BT> constexpr size_t big_lds_bytes() {
   constexpr size_t stages = (size_t(BT::NSA) * BT::BM + size_t(BT::NSB) * BT::BN) * 128;
