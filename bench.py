@@ -127,7 +127,7 @@ def mfma_roofline(flops: float, ms: float, peak: float = BF16_PEAK_TFLOPS) -> di
 # workloads (each returns a dict; the synthetic data follows BASELINE.json)
 
 
-def wl_rms_norm(steps, warmup, int_bits=32, frac_bits=16, T=16384, H=4096):
+def wl_rms_norm(steps, warmup, T=16384, H=4096):
     import torch
 
     from fxpr_vllm._kernels import rows as K
@@ -141,10 +141,10 @@ def wl_rms_norm(steps, warmup, int_bits=32, frac_bits=16, T=16384, H=4096):
     sets = [(x, r0.clone(), w) for _ in range(copies_for(nbytes))]
 
     def fn(xx, rr, ww):
-        return K.rms_norm_fxp_residual_run(xx, rr, ww, 1e-6, int_bits=int_bits, frac_bits=frac_bits)
+        return K.rms_norm_fxp_residual_run(xx, rr, ww, 1e-6)
 
     ms = time_op(fn, sets, steps, warmup)
-    return {"workload": f"rms_norm_residual bf16 [{T},{H}] Q{frac_bits}/i{int_bits}",
+    return {"workload": f"rms_norm_residual bf16 [{T},{H}]",
             "ms": round(ms, 5), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms)}
 
 
@@ -328,8 +328,7 @@ WORKLOADS = {
     "gemm_lm_head_m8192_i64": lambda s, w: wl_gemm(s, w, 8192, int_bits=64),
     "gemm_f16_14336_m8192": lambda s, w: wl_gemm(s, w, 8192, N=14336, dtype_name="f16"),
     "gemm_f32_14336_m8192": lambda s, w: wl_gemm(max(3, s // 4), 1, 8192, N=14336, dtype_name="f32"),
-    "rms_norm": lambda s, w: wl_rms_norm(s, w, 32, 16),
-    "rms_norm_q32i64": lambda s, w: wl_rms_norm(s, w, 64, 32),
+    "rms_norm": lambda s, w: wl_rms_norm(s, w),
     "log_softmax": lambda s, w: wl_log_softmax(s, w, 32, 16),
     "log_softmax_f32out_q32i64": lambda s, w: wl_log_softmax(s, w, 64, 32, fp32_out=True),
     "hbm_copy": lambda s, w: wl_hbm_copy(s, w),
@@ -380,14 +379,14 @@ def cpu_baseline(headline: str, budget_s: float) -> dict:
         w = np.full(H, 0x3F80, np.uint16)
         reps, t0 = 0, time.perf_counter()
         while True:
-            OR.rms_norm(x, w, 1e-6, "bf16", 32, 16, residual=r)
+            OR.rms_norm(x, w, 1e-6, "bf16", residual=r)
             reps += 1
             if time.perf_counter() - t0 > budget_s:
                 break
         dt = (time.perf_counter() - t0) / reps
         gbs = 4 * rows * H * 2 / dt / 1e9
         return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": f"oracle.rows.rms_norm bf16 [{rows},{H}] + residual, Q16/i32, "
+                "sample": f"oracle.rows.rms_norm bf16 [{rows},{H}] + residual, "
                           f"{reps} reps in {budget_s:.0f}s"}
     raise ValueError(headline)
 

@@ -84,26 +84,31 @@ int fxpr_fixed_row_sum(const void* q, int q_dtype, void* out, int int_bits,
 
 /*
  * Deterministic RMSNorm over contiguous [rows, hidden] rows of x (f32, f16
- * or bf16; weight and y share that type). With residual != NULL the fused
- * form runs: v = x + residual is written back into residual (rounded to the
- * I/O type) and normalised. The sum of squares is a fixed-point integer sum:
- * each fl32(v*v) is cast with float_to_fixed(int_bits, frac_bits) and the
- * row total is exact-then-saturated, so it is independent of the reduction
- * order. rrms = 1 / sqrt(total / hidden + eps) with IEEE sqrt and division,
- * y = IO((u * w) * rrms) where u is the (rounded) value that was stored.
+ * or bf16; weight and y share that type), hidden <= 2^22. With residual !=
+ * NULL the fused form runs: v = x + residual is written back into residual
+ * (rounded to the I/O type) and normalised. The sum of squares is an exact
+ * integer sum in a per-row block floating-point format: with 2^e <= max|v| <
+ * 2^(e+1), T = sum_j RNE(fl32(ldexp(v_j, -e)^2) * 2^40) in 64 bits (cannot
+ * overflow), mean_sq = ldexp(fl32(T) / hidden, 2e - 40), so the result is
+ * independent of the reduction order and does not saturate. rrms =
+ * 1 / sqrt(mean_sq + eps) with IEEE sqrt and division, y = IO((u * w) * rrms)
+ * where u is the (rounded) value that was stored. A row holding inf or NaN
+ * gets mean_sq = inf or NaN, as an fp32 sum would.
  * Replaces rms_norm_fxp_run / rms_norm_fxp_residual_run + _rms_norm_kernel
- * (fxpr_vllm/_triton/rms_norm.py:137-151, 78-134, 19-64).
+ * (fxpr_vllm/_triton/rms_norm.py:137-151, 78-134, 19-64), which take no
+ * fixed-point format either.
  */
 int fxpr_rms_norm(const void* x, void* residual, const void* weight, void* y,
                   int io_dtype, int64_t rows, int64_t hidden, float eps,
-                  int int_bits, int frac_bits, void* stream);
+                  void* stream);
 
 /*
  * Deterministic log-softmax over contiguous [rows, cols] rows of x (f32, f16
- * or bf16) into y (same type or f32). Per row: m = max x, e_j = exp(x_j - m)
- * by this library's fixed fp32 polynomial, S = exact-then-saturated sum of
- * float_to_fixed(e_j, int_bits, frac_bits), lse = m + log(S * 2^-frac_bits)
- * by the matching fixed polynomial, y_j = OUT(x_j - lse).
+ * or bf16) into y (same type or f32), cols < 2^31. Per row: m = max x,
+ * e_j = exp(x_j - m) by this library's fixed fp32 polynomial, S = exact sum
+ * (64- or 128-bit, never saturated) of float_to_fixed(e_j, int_bits,
+ * frac_bits), lse = m + log(fl32(S) * 2^-frac_bits) by the matching fixed
+ * polynomial, y_j = OUT(x_j - lse).
  * No counterpart kernel exists in the reference: it lists
  * fxpr_vllm/_triton/softmax.py (README.md:60) but does not ship it.
  */

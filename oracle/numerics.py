@@ -173,6 +173,41 @@ def sat_sum_nonneg(q: np.ndarray, int_bits: int, axis: int = -1) -> np.ndarray:
     return np.array(sums, dtype=np.int64).reshape(moved.shape[:-1])
 
 
+def int_to_f32(n: int) -> np.float32:
+    """fl32 of a non-negative Python integer of any size: round half to even
+    to 24 significant bits (inf beyond the fp32 range)."""
+    n = int(n)
+    if n < 0:
+        raise ValueError("int_to_f32 takes non-negative integers")
+    sh = n.bit_length() - 24
+    if sh > 0:
+        q, rem = divmod(n, 1 << sh)
+        half = 1 << (sh - 1)
+        if rem > half or (rem == half and q & 1):
+            q += 1
+        n = q << sh
+    with np.errstate(over="ignore"):
+        return np.float32(float(n)) if n < 2 ** 128 else np.float32(np.inf)
+
+
+def exact_sum_nonneg_f32(q: np.ndarray, axis: int = -1) -> tuple[np.ndarray, np.ndarray]:
+    """(S == 0, fl32(S)) for S the exact sum of non-negative int64 terms along
+    `axis`; numpy int64 sums where they cannot wrap, Python integers beyond."""
+    q = np.asarray(q, dtype=np.int64)
+    moved = np.moveaxis(q, axis, -1)
+    flat = moved.reshape(-1, moved.shape[-1])
+    n = flat.shape[-1]
+    top = int(flat.max()) if flat.size else 0
+    if top * n < (1 << 63):
+        s = flat.sum(axis=-1)
+        zero, f = s == 0, s.astype(np.float32)
+    else:
+        sums = [sum(int(v) for v in row) for row in flat]
+        zero = np.array([t == 0 for t in sums], dtype=bool)
+        f = np.array([int_to_f32(t) for t in sums], dtype=np.float32)
+    return zero.reshape(moved.shape[:-1]), f.reshape(moved.shape[:-1])
+
+
 # ---------------------------------------------------------------------------
 # The build's own exp and log (no reference counterpart: the reference's
 # log-softmax file is absent, fxpr_vllm README.md:60). Cody-Waite style

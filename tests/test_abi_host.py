@@ -46,7 +46,7 @@ def test_error_codes_without_gpu():
     assert lib.fxpr_float_to_fixed(None, 2, None, 32, 16, -1, None) == -3
     assert lib.fxpr_float_to_fixed(None, 1, ctypes.c_void_p(16), 32, 16, 0, None) == 0  # empty: no-op
     assert lib.fxpr_fixed_to_float(None, 4, None, 8, 16, 10, None) == -2
-    assert lib.fxpr_rms_norm(None, None, None, None, 2, 1, 8, 1e-6, 32, 16, None) == -5
+    assert lib.fxpr_rms_norm(None, None, None, None, 2, 1, 8, 1e-6, None) == -5
     assert lib.fxpr_log_softmax(None, 9, None, 9, 0, 8, 32, 16, None) == 0
     assert "out of range" in _hip.error_string(-2)
     assert _hip.error_string(-4).startswith("fxpr: workspace")

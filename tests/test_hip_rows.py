@@ -10,6 +10,7 @@ identity.
 from __future__ import annotations
 
 import json
+import math
 import pathlib
 
 import numpy as np
@@ -26,7 +27,6 @@ from tests._util import IO_NAME, from_np, mismatch_report, nan_aware_equal, seed
 pytestmark = pytest.mark.gpu
 KATS = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 DEV = "cuda"
-BITS = [(32, 16), (64, 32), (16, 8), (64, 16)]
 
 
 # --------------------------------------------------------------------------
@@ -82,50 +82,104 @@ def _rms_case(io_dtype, shape, seed, residual):
     return x, w, r
 
 
-def _rms_check(x, w, r, b, f, eps=1e-6):
+def _rms_check(x, w, r, eps=1e-6):
     io = IO_NAME[x.dtype]
     xd, wd = x.to(DEV), w.to(DEV)
     rd = r.to(DEV).clone() if r is not None else None
     if rd is None:
-        y = K.rms_norm_fxp_run(xd, wd, eps, int_bits=b, frac_bits=f)
+        y = K.rms_norm_fxp_run(xd, wd, eps)
     else:
-        y = K.rms_norm_fxp_residual_run(xd, rd, wd, eps, int_bits=b, frac_bits=f)
-    y_want, r_want = R.rms_norm(to_np(x), to_np(w), eps, io, b, f,
-                                residual=None if r is None else to_np(r))
+        y = K.rms_norm_fxp_residual_run(xd, rd, wd, eps)
+    y_want, r_want = R.rms_norm(to_np(x), to_np(w), eps, io, residual=None if r is None else to_np(r))
     y_want = from_np(y_want, x.dtype)
     assert nan_aware_equal(y.cpu(), y_want), mismatch_report(y.cpu(), y_want)
     if r is not None:
         r_want = from_np(r_want, x.dtype)
         assert nan_aware_equal(rd.cpu(), r_want), mismatch_report(rd.cpu(), r_want)
-    return y
+    return y, rd
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("residual", [False, True])
-@pytest.mark.parametrize("b,f", BITS)
+@pytest.mark.parametrize("scale", [1.0, 30.0])
 @pytest.mark.parametrize("shape", [(64, 4096), (3, 7), (1, 1), (2, 40_000), (17, 1000)])
-def test_rms_norm_bit_exact(dtype, residual, b, f, shape):
-    x, w, r = _rms_case(dtype, shape, seed=hash((shape, b)) % 1000, residual=residual)
-    _rms_check(x, w, r, b, f)
+def test_rms_norm_bit_exact(dtype, residual, scale, shape):
+    # (2, 40000) is longer than the register cache: its tail is re-read and
+    # its residual written back in the sum pass
+    x, w, r = _rms_case(dtype, shape, seed=shape[-1] % 1000, residual=residual)
+    x = (x.float() * scale).to(dtype)
+    _rms_check(x, w, r)
 
 
-def test_rms_norm_op_uses_runtime_config(monkeypatch):
+def _realistic_rows(H=4096, seed=0):
+    """RMS 3, 5, 20, 100, 1e4 and 1e-3 rows, plus an N(0, 0.5) row with one
+    channel at 1500 (residual-stream magnitudes where a Q16.16 int32 sum of
+    squares would saturate)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    rows = [torch.randn(H, generator=g) * s for s in (3.0, 5.0, 20.0, 100.0, 1.0e4, 1.0e-3)]
+    spike = torch.randn(H, generator=g) * 0.5
+    spike[H // 3] = 1500.0
+    return torch.stack(rows + [spike])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("residual", [False, True])
+def test_rms_norm_realistic_magnitudes(dtype, residual):
+    # bit-exact vs the oracle, and within the reference's own tolerances
+    # (fxpr_vllm/_tests/test_rms_norm.py: 2e-2 bf16, 5e-3 f16, 5e-4 fp32) of
+    # the reference's fp32 RMSNorm (_triton/rms_norm.py:38-64)
+    x = _realistic_rows().to(dtype)
+    r = (_realistic_rows(seed=1) * 0.5).to(dtype) if residual else None
+    w = seeded((4096,), 7, std=0.1, mean=1.0, dtype=dtype)
+    y, rd = _rms_check(x, w, r)
+    v = x.double() + (r.double() if residual else 0.0)
+    u = rd.cpu().double() if residual else x.double()
+    ref = u * w.double() / torch.sqrt((v * v).mean(-1, keepdim=True) + 1e-6)
+    ref = ref.float().to(dtype).double()
+    tol = _TOL[dtype]
+    assert torch.allclose(y.cpu().double(), ref, atol=tol, rtol=tol)
+
+
+def test_rms_norm_special_rows():
+    # zero, subnormal, subnormal mean square, fp32-overflowing mean square,
+    # inf and NaN rows (eps 1e-6 and 0)
+    H = 64
+    x = torch.zeros(6, H)
+    x[1] = 2.0 ** -140
+    x[2] = 2.0 ** -70
+    x[3] = 1.0e30
+    x[4, 0], x[4, 1:] = float("inf"), 1.0
+    x[5, 0], x[5, 1:] = float("nan"), 1.0
+    w = torch.full((H,), 2.0)
+    for eps in (1e-6, 0.0):
+        for rows in (x, x.repeat(1, 1000)[:, : H * 1000]):
+            ww = w.repeat(rows.shape[1] // H)
+            _rms_check(rows, ww, None, eps=eps)
+            _rms_check(rows, ww, torch.zeros_like(rows), eps=eps)
+
+
+def test_rms_norm_ignores_fixed_point_knobs(monkeypatch):
+    # like the reference's RMSNorm, the op takes no fixed-point format: the
+    # FXPR_* knobs (which the GEMM and attention read) do not change its bits
     x, w, r = _rms_case(torch.bfloat16, (8, 4096), 5, True)
-    for b, f in ((32, 16), (64, 32)):
+    outs = []
+    for b, f in ((32, 16), (64, 32), (16, 8)):
         monkeypatch.setenv("FXPR_INT_BITS", str(b))
         monkeypatch.setenv("FXPR_FRAC_BITS", str(f))
         fxpr_config.reset_runtime_config()
         try:
             rd = r.to(DEV).clone()
             y = torch.ops.fxpr.rms_norm_fxp_residual(x.to(DEV), rd, w.to(DEV), 1e-6)
-            y_want, r_want = R.rms_norm(to_np(x), to_np(w), 1e-6, "bf16", b, f, residual=to_np(r))
-            assert torch.equal(y.cpu(), from_np(y_want, torch.bfloat16))
-            assert torch.equal(rd.cpu(), from_np(r_want, torch.bfloat16))
             y2 = torch.ops.fxpr.rms_norm_fxp(x.to(DEV), w.to(DEV), 1e-6)
-            assert torch.equal(y2.cpu(), from_np(R.rms_norm(to_np(x), to_np(w), 1e-6, "bf16", b, f)[0],
-                                                 torch.bfloat16))
+            outs.append((y.cpu(), rd.cpu(), y2.cpu()))
         finally:
             fxpr_config.reset_runtime_config()
+    y_want, r_want = R.rms_norm(to_np(x), to_np(w), 1e-6, "bf16", residual=to_np(r))
+    y2_want, _ = R.rms_norm(to_np(x), to_np(w), 1e-6, "bf16")
+    for y, rd, y2 in outs:
+        assert torch.equal(y, from_np(y_want, torch.bfloat16))
+        assert torch.equal(rd, from_np(r_want, torch.bfloat16))
+        assert torch.equal(y2, from_np(y2_want, torch.bfloat16))
 
 
 def test_rms_norm_noncontiguous_residual_copy_back():
@@ -134,7 +188,7 @@ def test_rms_norm_noncontiguous_residual_copy_back():
     r_nc = base.to(DEV).t()  # [6, 64] non-contiguous view
     r_host = base.t().contiguous()
     y = torch.ops.fxpr.rms_norm_fxp_residual(x.to(DEV), r_nc, w.to(DEV), 1e-6)
-    y_want, r_want = R.rms_norm(to_np(x), to_np(w), 1e-6, "f16", 32, 16, residual=to_np(r_host))
+    y_want, r_want = R.rms_norm(to_np(x), to_np(w), 1e-6, "f16", residual=to_np(r_host))
     assert torch.equal(y.cpu(), from_np(y_want, torch.float16))
     assert torch.equal(r_nc.cpu(), from_np(r_want, torch.float16))
 
@@ -142,13 +196,13 @@ def test_rms_norm_noncontiguous_residual_copy_back():
 def test_rms_norm_batch_invariance():
     x, w, r = _rms_case(torch.bfloat16, (128, 4096), 21, True)
     xd, wd = x.to(DEV), w.to(DEV)
-    full = K.rms_norm_fxp_run(xd, wd, 1e-6, 32, 16)
+    full = K.rms_norm_fxp_run(xd, wd, 1e-6)
     for row in (0, 3, 17, 64, 127):
         for batch in (1, 4, 16, 128):
             if row >= batch:
                 continue
             sub = xd[:batch].clone()
-            out = K.rms_norm_fxp_run(sub, wd, 1e-6, 32, 16)
+            out = K.rms_norm_fxp_run(sub, wd, 1e-6)
             assert torch.equal(out[row], full[row])
 
 
@@ -252,11 +306,12 @@ def test_log_softmax_special_rows():
 
 
 @pytest.mark.parametrize("b,f", [(32, 16), (16, 8), (16, 16), (32, 32)])
-def test_log_softmax_saturating_sums_and_exact_path(b, f):
-    # rows whose fixed-point denominator saturates (flat rows: every term is
-    # 2^f), next to ordinary rows; (16, 16) and (32, 32) take the exact
-    # per-term path (a term can exceed the rounding constant's range or qmax),
-    # (32, 16) and (16, 8) the rounding-constant one with 32-bit lane sums
+def test_log_softmax_wide_sums_and_exact_path(b, f):
+    # flat rows whose denominator V * 2^f exceeds the term width (the sum is
+    # exact and unclamped), next to ordinary rows; (16, 16) and (32, 32) take
+    # the exact per-term path (a term can exceed the rounding constant's range
+    # or qmax), (32, 16) and (16, 8) the rounding-constant one with 32-bit
+    # lane sums
     x = _logits(6, 128_256, seed=b * f)
     x[0] = 0.0
     x[1] = -3.5
@@ -271,6 +326,28 @@ def test_log_softmax_close_to_torch():
     got = torch.ops.fxpr.log_softmax_fxp(x.to(DEV), 64, 32).cpu()
     ref = torch.log_softmax(x.double(), dim=-1)
     assert torch.allclose(got.double(), ref, atol=1e-4, rtol=1e-5)
+
+
+@pytest.mark.parametrize("b,f", [(32, 16), (16, 8), (64, 32), (64, 63), (32, 0)])
+def test_log_softmax_flat_full_vocab_row(b, f):
+    # a flat [V = 128256] row: V * 2^f exceeds the knob's width, the exact
+    # denominator does not saturate (128-bit for (64, 63)), y = -ln V
+    V = 128_256
+    x = torch.zeros(3, V, dtype=torch.bfloat16)
+    x[1] = 5.0
+    x[2, : V // 2] = -1.0
+    # the launcher (the op admits frac bits 8 / 16 / 32 only, fxpr_vllm/_lib.py:55-56)
+    for out_dtype in (None, torch.float32):
+        got = K.log_softmax_fxp_run(x.to(DEV), b, f, out_dtype).cpu()
+        want = from_np(R.log_softmax(to_np(x), "bf16", IO_NAME[out_dtype or x.dtype], b, f), out_dtype or x.dtype)
+        assert nan_aware_equal(got, want), mismatch_report(got, want)
+    got = K.log_softmax_fxp_run(x.to(DEV), b, f, torch.float32).cpu()
+    assert abs(got[0, 0].item() + math.log(V)) < 4e-6 * math.log(V)
+    assert abs(got[1, 0].item() + math.log(V)) < 4e-6 * math.log(V)
+    # the exp of the output sums to 1 up to the quantisation of the terms
+    # (each term is off by at most 2^-(f+1) of the row maximum's weight)
+    if f >= 16:
+        assert abs(torch.exp(got.double()).sum(-1) - 1).max().item() < V * 2.0 ** -(f + 1) + 1e-5
 
 
 def test_log_softmax_batch_and_run_invariance():
@@ -289,7 +366,6 @@ def test_rms_norm_rrms_correctly_rounded():
     c = torch.exp(torch.rand(20_000, generator=g) * 12 - 6)
     x = c[:, None].expand(20_000, 64).contiguous()
     w = torch.ones(64)
-    for b, f in ((64, 32), (32, 16)):
-        y = K.rms_norm_fxp_run(x.to(DEV), w.to(DEV), 1e-6, int_bits=b, frac_bits=f).cpu()
-        want = torch.from_numpy(R.rms_norm(x.numpy(), w.numpy(), 1e-6, "f32", b, f)[0])
-        assert torch.equal(y, want), mismatch_report(y, want)
+    y = K.rms_norm_fxp_run(x.to(DEV), w.to(DEV), 1e-6).cpu()
+    want = torch.from_numpy(R.rms_norm(x.numpy(), w.numpy(), 1e-6, "f32")[0])
+    assert torch.equal(y, want), mismatch_report(y, want)

@@ -125,16 +125,6 @@ __device__ __forceinline__ float fixed_to_f32(int32_t q, float inv_scale) {
 }
 
 // ---------------------------------------------------------------------------
-// Saturating sums of non-negative fixed-point terms. For values in [0, qmax]
-// min(a + b, qmax) is associative and commutative (it equals the exact sum
-// clamped once), so any reduction tree gives the same bits. Terms are below
-// 2^63, so a pairwise sum always fits in uint64.
-__device__ __forceinline__ uint64_t sat_add_nonneg(uint64_t a, uint64_t b, uint64_t qmax) {
-  uint64_t s = a + b;
-  return s > qmax ? qmax : s;
-}
-
-// ---------------------------------------------------------------------------
 // The library's own exp and log (used where results must be reproducible on
 // the CPU bit for bit). Method: Cody-Waite style reduction to a power of two
 // plus a Taylor polynomial evaluated by Horner's rule, one rounding per
@@ -223,12 +213,6 @@ template <typename T> __device__ __forceinline__ T wave_max(T v) {
     T w = __shfl_xor(v, o, 64);
     v = v > w ? v : w;
   }
-  return v;
-}
-
-__device__ __forceinline__ uint64_t wave_sat_sum(uint64_t v, uint64_t qmax) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = sat_add_nonneg(v, __shfl_xor(v, o, 64), qmax);
   return v;
 }
 

@@ -3,9 +3,9 @@
 //
 // One workgroup owns one row, so a row never depends on its neighbours
 // (batch invariance). Within the row every partial is an integer and the
-// cross-lane / cross-wave combine is an exact (or, for non-negative terms,
-// saturating-and-therefore-associative) integer sum, so the bits do not
-// depend on the workgroup size or the reduction tree either. Rows are
+// cross-lane / cross-wave combine is an exact integer sum (saturated once at
+// the end where the op saturates), so the bits do not depend on the
+// workgroup size or the reduction tree either. Rows are
 // streamed with 16-byte vector loads and, up to NREG vectors per thread, kept
 // in registers between the reduction pass and the output pass so x is read
 // from HBM once.
@@ -47,14 +47,28 @@ __device__ float block_max(float v, float* smem) {
   return r;
 }
 
-__device__ uint64_t block_sat_sum(uint64_t v, uint64_t qmax, uint64_t* smem) {
-  v = wave_sat_sum(v, qmax);
+using u128 = unsigned __int128;
+
+__device__ __forceinline__ u128 shfl_xor_u128(u128 v, int o) {
+  uint64_t lo = static_cast<uint64_t>(v), hi = static_cast<uint64_t>(v >> 64);
+  lo = __shfl_xor(lo, o, 64);
+  hi = __shfl_xor(hi, o, 64);
+  return (static_cast<u128>(hi) << 64) | lo;
+}
+
+// Exact workgroup sum of unsigned 64- or 128-bit lane values.
+template <class U> __device__ U block_exact_sum(U v, U* smem) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    if constexpr (sizeof(U) == 16) v += shfl_xor_u128(v, o);
+    else v += __shfl_xor(v, o, 64);
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   __syncthreads();
   if (lane == 0) smem[wave] = v;
   __syncthreads();
-  uint64_t r = smem[0];
-  for (int w = 1; w < nw; ++w) r = sat_add_nonneg(r, smem[w], qmax);
+  U r = smem[0];
+  for (int w = 1; w < nw; ++w) r += smem[w];
   return r;
 }
 
@@ -70,7 +84,7 @@ template <int BITS> __device__ __forceinline__ uint64_t quant_nonneg(float s) {
   if constexpr (BITS == 64) {
     // RNE, then split r = h 2^32 + l exactly (r integral, h = floor(r 2^-32));
     // branch-free, so arrays of row values around it stay in registers.
-    // NaN -> 0; r >= 2^63 -> qmax (the caller's saturating add needs b <= qmax).
+    // NaN -> 0; r >= 2^63 -> qmax.
     const float r = __builtin_rintf(s);
     const float h = __builtin_floorf(__fmul_rn(r, 2.3283064365386963e-10f));
     const float l = __fsub_rn(r, __fmul_rn(h, 4294967296.0f));
@@ -140,11 +154,46 @@ int launch_row_sum(const void* q, void* out, int obits, int64_t rows, int64_t co
 // ---------------------------------------------------------------------------
 // RMSNorm(+residual).
 //
-// Pass 1 (per element j of the row): v = fl32(x) [+ fl32(r)]; with a residual
-// store r <- IO(v); add float_to_fixed(fl32(v*v)) to a saturating unsigned
-// accumulator. Row total T (exact sum clamped to qmax).
-// rrms = 1 / sqrt(fl32(T) * 2^-f / H + eps).
+// The sum of squares is an integer sum in a per-row block floating-point
+// format, so it is independent of the reduction order and cannot overflow:
+//   e   = exponent of the row's largest |v| (2^e <= max |v| < 2^(e+1); -126
+//         for a zero or subnormal maximum), found as the largest magnitude
+//         bit pattern (an exact integer maximum);
+//   q_j = RNE(fl32(s_j * s_j) * 2^40) with s_j = ldexp(v_j, -e), |s_j| < 2,
+//         so q_j < 2^42 and the 64-bit sum of up to 2^22 terms cannot wrap;
+//   mean_sq = ldexp(fl32(T) / H, 2e - 40), one rounding per step;
+//   rrms = 1 / sqrt(mean_sq + eps) (IEEE sqrt and division).
+// A row whose largest magnitude is inf or NaN takes mean_sq = that value.
+// Pass 1 (per element j): v = fl32(x) [+ fl32(r)], kept in registers for the
+// register-cached part of the row (the sum needs the unrounded v after the
+// row maximum is known); with a residual r <- IO(v).
 // Pass 2: u = fl32(IO(v)) (what was stored) or fl32(x); y = IO((u * w) * rrms).
+
+constexpr int kRmsSumFrac = 40;
+constexpr int64_t kRmsMaxHidden = int64_t(1) << 22;
+
+// q = RNE(t * 2^40) for 0 <= t < 4: fl64(t * 2^40 + 1.5 * 2^52) holds
+// 2^51 + q in its mantissa field (t * 2^40 is exact in fp64 and below 2^42;
+// in [2^52, 2^53) the spacing is 1 and the constant is even, so the fma's
+// one rounding is RNE with ties to even).
+__device__ __forceinline__ uint64_t rms_sq_term(float v, int neg_e) {
+  const float s = __builtin_ldexpf(v, neg_e);
+  const float t = __fmul_rn(s, s);
+  const double d = __builtin_fma(static_cast<double>(t), 1099511627776.0, 6755399441055744.0);
+  return static_cast<uint64_t>(__builtin_bit_cast(int64_t, d)) & ((uint64_t(1) << 51) - 1);
+}
+
+__device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7fffffffu; }
+
+__device__ uint32_t block_max_u32(uint32_t v, uint32_t* smem) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) smem[wave] = v;
+  __syncthreads();
+  uint32_t r = smem[0];
+  for (int w = 1; w < nw; ++w) r = r > smem[w] ? r : smem[w];
+  return r;
+}
 
 // Streamed rows are read and written once: non-temporal 16-byte accesses
 // (global_load/store ... nt) keep them from displacing reused lines in the
@@ -163,14 +212,15 @@ template <class V> __device__ __forceinline__ void nt_store(V* p, const V& v) {
     *p = v;
 }
 
-template <int DT, int VEC, int NREG, int BITS, bool RES>
+template <int DT, int VEC, int NREG, bool RES>
 __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
     const typename Io<DT>::T* __restrict__ x, typename Io<DT>::T* __restrict__ r,
     const typename Io<DT>::T* __restrict__ w, typename Io<DT>::T* __restrict__ y,
-    int64_t hidden, float eps, float scale, float inv_scale, uint64_t qmax) {
+    int64_t hidden, float eps) {
   using T = typename Io<DT>::T;
   using V = Vec<T, VEC>;
-  __shared__ uint64_t red[kMaxThreads / 64];
+  __shared__ uint32_t mred[kMaxThreads / 64];
+  __shared__ uint64_t sred[kMaxThreads / 64];
 
   const int64_t row = blockIdx.x;
   const int64_t nchunks = hidden / VEC;
@@ -181,46 +231,71 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
   const V* wr = reinterpret_cast<const V*>(w);
   V* yr = reinterpret_cast<V*>(y + row * hidden);
 
-  float keep[NREG][VEC];
-  uint64_t acc = 0;
-
-  auto pass1 = [&](int64_t c, float (&u)[VEC]) {
+  // v = fl32(x) [+ fl32(r)] of one chunk
+  auto load_v = [&](int64_t c, float (&v)[VEC]) {
     V xv = nt_load(xr + c);
-    float v[VEC];
 #pragma unroll
     for (int j = 0; j < VEC; ++j) v[j] = Io<DT>::load(xv.v[j]);
     if constexpr (RES) {
       V rv = nt_load(rr + c);
-      V sv;
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        v[j] = __fadd_rn(v[j], Io<DT>::load(rv.v[j]));
-        sv.v[j] = Io<DT>::store(v[j]);
-        u[j] = Io<DT>::load(sv.v[j]);
-      }
-      nt_store(rr + c, sv);
-    } else {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) u[j] = v[j];
+      for (int j = 0; j < VEC; ++j) v[j] = __fadd_rn(v[j], Io<DT>::load(rv.v[j]));
     }
+  };
+  auto store_r = [&](int64_t c, const float (&v)[VEC]) {
+    V sv;
 #pragma unroll
-    for (int j = 0; j < VEC; ++j)
-      acc = sat_add_nonneg(acc, quant_nonneg<BITS>(__fmul_rn(__fmul_rn(v[j], v[j]), scale)), qmax);
+    for (int j = 0; j < VEC; ++j) sv.v[j] = Io<DT>::store(v[j]);
+    nt_store(rr + c, sv);
   };
 
+  float keep[NREG][VEC];
+  uint32_t mx = 0;
 #pragma unroll
   for (int i = 0; i < NREG; ++i) {
     const int64_t c = tid + static_cast<int64_t>(i) * nthr;
-    if (c < nchunks) pass1(c, keep[i]);
+    if (c < nchunks) {
+      load_v(c, keep[i]);
+      if constexpr (RES) store_r(c, keep[i]);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) mx = max(mx, abs_bits(keep[i][j]));
+    }
   }
+  // rows longer than the register cache: the residual is written back in the
+  // sum pass, after v has been formed from the old residual a second time
   for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) {
-    float u[VEC];
-    pass1(c, u);
+    float v[VEC];
+    load_v(c, v);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) mx = max(mx, abs_bits(v[j]));
   }
 
-  const uint64_t total = block_sat_sum(acc, qmax, red);
-  float ms = div_rn(fixed_to_f32(static_cast<int64_t>(total), inv_scale), static_cast<float>(hidden));
-  ms = ms > 0.0f ? ms : 0.0f;
+  const uint32_t mbits = block_max_u32(mx, mred);
+  const int biased = static_cast<int>(mbits >> 23);
+  const int e = (biased > 1 ? biased : 1) - 127;
+  const int neg_e = -e;
+
+  uint64_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+    if (c < nchunks) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc += rms_sq_term(keep[i][j], neg_e);
+    }
+  }
+  for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) {
+    float v[VEC];
+    load_v(c, v);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) acc += rms_sq_term(v[j], neg_e);
+    if constexpr (RES) store_r(c, v);
+  }
+
+  const uint64_t total = block_exact_sum(acc, sred);
+  float ms = __builtin_ldexpf(div_rn(static_cast<float>(total), static_cast<float>(hidden)),
+                              2 * e - kRmsSumFrac);
+  if (mbits >= 0x7f800000u) ms = __uint_as_float(mbits);  // inf or NaN
   const float rrms = div_rn(1.0f, sqrt_rn(__fadd_rn(ms, eps)));
 
   auto pass2 = [&](int64_t c, const float (&u)[VEC]) {
@@ -235,7 +310,12 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
 #pragma unroll
   for (int i = 0; i < NREG; ++i) {
     const int64_t c = tid + static_cast<int64_t>(i) * nthr;
-    if (c < nchunks) pass2(c, keep[i]);
+    if (c < nchunks) {
+      float u[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) u[j] = RES ? Io<DT>::load(Io<DT>::store(keep[i][j])) : keep[i][j];
+      pass2(c, u);
+    }
   }
   for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) {
     V src = RES ? rr[c] : xr[c];  // residual already holds IO(v)
@@ -254,54 +334,45 @@ inline int threads_for(int64_t nchunks, int per_thread, int max_threads = kMaxTh
   return static_cast<int>(t);
 }
 
-template <int DT, int VEC, int BITS>
-int launch_rms_bits(const void* x, void* r, const void* w, void* y, int64_t rows, int64_t hidden,
-                    float eps, float scale, float inv, uint64_t qmax, hipStream_t st) {
+template <int DT, int VEC>
+int launch_rms_vec(const void* x, void* r, const void* w, void* y, int64_t rows, int64_t hidden,
+                   float eps, hipStream_t st) {
   using T = typename Io<DT>::T;
   constexpr int NREG = 4;
   const int64_t nchunks = hidden / VEC;
   const int nthr = threads_for(nchunks, 2);
   dim3 grid(static_cast<unsigned>(rows));
   if (r)
-    rms_norm_kernel<DT, VEC, NREG, BITS, true><<<grid, nthr, 0, st>>>(
+    rms_norm_kernel<DT, VEC, NREG, true><<<grid, nthr, 0, st>>>(
         static_cast<const T*>(x), static_cast<T*>(r), static_cast<const T*>(w), static_cast<T*>(y),
-        hidden, eps, scale, inv, qmax);
+        hidden, eps);
   else
-    rms_norm_kernel<DT, VEC, NREG, BITS, false><<<grid, nthr, 0, st>>>(
-        static_cast<const T*>(x), nullptr, static_cast<const T*>(w), static_cast<T*>(y),
-        hidden, eps, scale, inv, qmax);
+    rms_norm_kernel<DT, VEC, NREG, false><<<grid, nthr, 0, st>>>(
+        static_cast<const T*>(x), nullptr, static_cast<const T*>(w), static_cast<T*>(y), hidden, eps);
   return launch_status();
 }
 
 template <int DT>
 int launch_rms(const void* x, void* r, const void* w, void* y, int64_t rows, int64_t hidden,
-               float eps, int bits, int frac, hipStream_t st) {
+               float eps, hipStream_t st) {
   using T = typename Io<DT>::T;
   constexpr int VEC = 16 / sizeof(T);
-  const float scale = pow2f(frac), inv = pow2f(-frac);
-  const uint64_t qmax = qmax_for_bits(bits);
   const bool vec_ok = hidden % VEC == 0 && aligned(x, 16) && aligned(w, 16) && aligned(y, 16) &&
                       (!r || aligned(r, 16));
-#define FXPR_RMS_CASE(V, B) \
-  return launch_rms_bits<DT, V, B>(x, r, w, y, rows, hidden, eps, scale, inv, qmax, st)
-  if (vec_ok) {
-    if (bits == 16) FXPR_RMS_CASE(VEC, 16);
-    if (bits == 32) FXPR_RMS_CASE(VEC, 32);
-    FXPR_RMS_CASE(VEC, 64);
-  } else {
-    if (bits == 16) FXPR_RMS_CASE(1, 16);
-    if (bits == 32) FXPR_RMS_CASE(1, 32);
-    FXPR_RMS_CASE(1, 64);
-  }
-#undef FXPR_RMS_CASE
+  if (vec_ok) return launch_rms_vec<DT, VEC>(x, r, w, y, rows, hidden, eps, st);
+  return launch_rms_vec<DT, 1>(x, r, w, y, rows, hidden, eps, st);
 }
 
 // ---------------------------------------------------------------------------
 // Log-softmax.
 //
 // Pass 1: m = max_j fl32(x_j) (NaN propagates).
-// Pass 2: S = sat-sum_j RNE_sat(exp_scaled(fl32(x_j) - m, f)).
-// lse = m + ln(fl32(S) * 2^-f) (ln by log_own; S == 0 gives -inf).
+// Pass 2: S = exact sum_j RNE_sat_b(exp_scaled(fl32(x_j) - m, f)). The terms
+// saturate at the knob's width, the sum never does: it is a 64-bit integer
+// (128-bit when cols * the largest term could reach 2^64), so a near-flat
+// full-vocabulary row still normalises.
+// lse = m + ln(fl32(S) * 2^-f) (fl32 correctly rounded; ln by log_own; S == 0
+// gives -inf).
 // Pass 3: y_j = OUT(fl32(x_j) - lse).
 
 // Log-softmax workgroups are at most 512 threads (two waves per SIMD), so a
@@ -325,20 +396,34 @@ __device__ __forceinline__ uint32_t exp_scaled_rc_bits(float d, int f) {
   return __float_as_uint(__builtin_fmaf(exp2_poly(r), s2, 12582912.0f));
 }
 
+// fl32(v), round half to even, for an unsigned 64- or 128-bit integer. A
+// 128-bit value beyond 64 bits is shifted into 64 bits with the dropped bits
+// ORed into bit 0 (they lie far below the 24-bit rounding position, so only a
+// tie can depend on them), converted, and scaled back exactly.
+__device__ __forceinline__ float uint_to_f32(uint64_t v) { return static_cast<float>(v); }
+__device__ __forceinline__ float uint_to_f32(u128 v) {
+  const uint64_t hi = static_cast<uint64_t>(v >> 64);
+  if (hi == 0) return static_cast<float>(static_cast<uint64_t>(v));
+  const int n = 64 - __builtin_clzll(hi);
+  const u128 dropped = v & ((static_cast<u128>(1) << n) - 1);
+  const uint64_t top = static_cast<uint64_t>(v >> n) | (dropped != 0 ? 1u : 0u);
+  return __builtin_ldexpf(static_cast<float>(top), n);
+}
+
 // The per-lane sums of the rounding-constant path are plain 32-bit adds: the
 // host enables it only when elements per lane x the largest term stay below
-// 2^32, and one clamp of the exact sum equals the saturating sum of
-// non-negative terms.
-template <int XDT, int YDT, int VEC, int NREG, int BITS>
+// 2^32. WIDE (64-bit terms only) takes 128-bit sums.
+template <int XDT, int YDT, int VEC, int NREG, int BITS, bool WIDE>
 __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
     const typename Io<XDT>::T* __restrict__ x, typename Io<YDT>::T* __restrict__ y, int64_t cols,
-    int frac, float inv_scale, uint64_t qmax, int fast_sum) {
+    int frac, float inv_scale, int fast_sum) {
   using XT = typename Io<XDT>::T;
   using YT = typename Io<YDT>::T;
   using XV = Vec<XT, VEC>;
   using YV = Vec<YT, VEC>;
+  using SumT = typename std::conditional<WIDE, u128, uint64_t>::type;
   __shared__ float fred[kLsmThreads / 64];
-  __shared__ uint64_t ired[kLsmThreads / 64];
+  __shared__ SumT ired[kLsmThreads / 64];
 
   const int64_t row = blockIdx.x;
   const int64_t nchunks = cols / VEC;
@@ -368,21 +453,12 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
   }
   m = block_max(m, fred);
 
-  // Terms are in [0, qmax]; for qmax < 2^31 a 32-bit min(a + b, qmax) is
-  // the same saturating sum as the 64-bit one.
-  using SumT = typename std::conditional<BITS == 64, uint64_t, uint32_t>::type;
   SumT acc = 0;
   auto accum = [&](const XV& xv) {
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
       const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
-      const uint64_t q = quant_nonneg<BITS>(exp_scaled_to_round(d, frac));
-      if constexpr (BITS == 64) {
-        acc = sat_add_nonneg(acc, q, qmax);
-      } else {
-        const uint32_t s32 = acc + static_cast<uint32_t>(q);
-        acc = s32 < static_cast<uint32_t>(qmax) ? s32 : static_cast<uint32_t>(qmax);
-      }
+      acc += static_cast<SumT>(quant_nonneg<BITS>(exp_scaled_to_round(d, frac)));
     }
   };
   if (BITS != 64 && fast_sum) {
@@ -398,7 +474,7 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
       if (c < nchunks) accum_rc(keep[i]);
     }
     for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum_rc(xr[c]);
-    acc = static_cast<SumT>(acc32 < qmax ? acc32 : qmax);
+    acc = acc32;
   } else {
 #pragma unroll
     for (int i = 0; i < NREG; ++i) {
@@ -414,10 +490,9 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
 #pragma unroll
     for (int i = 0; i < NREG; ++i) asm volatile("" : "+v"(keep[i].v));
   }
-  const uint64_t total = block_sat_sum(static_cast<uint64_t>(acc), qmax, ired);
+  const SumT total = block_exact_sum(acc, ired);
 
-  const float lnS = total == 0 ? -__builtin_inff()
-                               : log_own(fixed_to_f32(static_cast<int64_t>(total), inv_scale));
+  const float lnS = total == 0 ? -__builtin_inff() : log_own(__fmul_rn(uint_to_f32(total), inv_scale));
   const float lse = __fadd_rn(m, lnS);
 
   auto emit = [&](int64_t c, const XV& xv) {
@@ -443,22 +518,26 @@ int launch_lsm_vec(const void* x, void* y, int64_t rows, int64_t cols, int bits,
   const int64_t nchunks = cols / VEC;
   const int nthr = threads_for(nchunks, NREG, kLsmThreads);
   const float inv = pow2f(-frac);
-  const uint64_t qmax = qmax_for_bits(bits);
+  const double qmax = double(qmax_for_bits(bits));
+  // the largest term: e^0 * 2^f, with margin for the polynomial, or qmax
+  const double term_max = std::fmin(1.4143 * std::ldexp(1.0, frac) + 1.0, qmax);
   // rounding-constant sums: 1.4143 * 2^f below 2^22 and qmax, and a lane's
-  // terms (each at most 1.4143 * 2^f) summing below 2^32
-  const double term_max = 1.4143 * std::ldexp(1.0, frac) + 1.0;
+  // terms summing below 2^32
   const double lane_elems = double(cdiv(nchunks, nthr)) * VEC;
-  const int fast = bits != 64 && term_max < 4194304.0 && term_max <= double(qmax) &&
+  const int fast = bits != 64 && term_max < 4194304.0 && term_max < qmax &&
                    lane_elems * term_max < 4294967296.0;
+  const bool wide = double(cols) * term_max >= 18446744073709551616.0;
   dim3 grid(static_cast<unsigned>(rows));
   const XT* xp = static_cast<const XT*>(x);
   YT* yp = static_cast<YT*>(y);
   if (bits == 16)
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 16><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax, fast);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 16, false><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, fast);
   else if (bits == 32)
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 32><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax, fast);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 32, false><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, fast);
+  else if (!wide)
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 64, false><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, 0);
   else
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 64><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, qmax, fast);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 64, true><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, 0);
   return launch_status();
 }
 
@@ -493,17 +572,15 @@ extern "C" int fxpr_fixed_row_sum(const void* q, int q_dtype, void* out, int int
 }
 
 extern "C" int fxpr_rms_norm(const void* x, void* residual, const void* weight, void* y,
-                             int io_dtype, int64_t rows, int64_t hidden, float eps, int int_bits,
-                             int frac_bits, void* stream) {
-  if (!valid_int_bits(int_bits) || frac_bits < 0 || frac_bits > 63) return FXPR_E_BITS;
-  if (rows < 0 || hidden < 0 || rows > 0x7fffffff) return FXPR_E_SHAPE;
+                             int io_dtype, int64_t rows, int64_t hidden, float eps, void* stream) {
+  if (rows < 0 || hidden < 0 || rows > 0x7fffffff || hidden > kRmsMaxHidden) return FXPR_E_SHAPE;
   if (rows == 0 || hidden == 0) return FXPR_OK;
   if (!x || !weight || !y) return FXPR_E_ARG;
   hipStream_t st = as_stream(stream);
   switch (io_dtype) {
-    case FXPR_DTYPE_F16: return launch_rms<FXPR_DTYPE_F16>(x, residual, weight, y, rows, hidden, eps, int_bits, frac_bits, st);
-    case FXPR_DTYPE_BF16: return launch_rms<FXPR_DTYPE_BF16>(x, residual, weight, y, rows, hidden, eps, int_bits, frac_bits, st);
-    case FXPR_DTYPE_F32: return launch_rms<FXPR_DTYPE_F32>(x, residual, weight, y, rows, hidden, eps, int_bits, frac_bits, st);
+    case FXPR_DTYPE_F16: return launch_rms<FXPR_DTYPE_F16>(x, residual, weight, y, rows, hidden, eps, st);
+    case FXPR_DTYPE_BF16: return launch_rms<FXPR_DTYPE_BF16>(x, residual, weight, y, rows, hidden, eps, st);
+    case FXPR_DTYPE_F32: return launch_rms<FXPR_DTYPE_F32>(x, residual, weight, y, rows, hidden, eps, st);
     default: return FXPR_E_DTYPE;
   }
 }
@@ -511,7 +588,7 @@ extern "C" int fxpr_rms_norm(const void* x, void* residual, const void* weight, 
 extern "C" int fxpr_log_softmax(const void* x, int x_dtype, void* y, int y_dtype, int64_t rows,
                                 int64_t cols, int int_bits, int frac_bits, void* stream) {
   if (!valid_int_bits(int_bits) || frac_bits < 0 || frac_bits > 63) return FXPR_E_BITS;
-  if (rows < 0 || cols < 0 || rows > 0x7fffffff) return FXPR_E_SHAPE;
+  if (rows < 0 || cols < 0 || rows > 0x7fffffff || cols > 0x7fffffff) return FXPR_E_SHAPE;
   if (rows == 0 || cols == 0) return FXPR_OK;
   if (!x || !y) return FXPR_E_ARG;
   hipStream_t st = as_stream(stream);

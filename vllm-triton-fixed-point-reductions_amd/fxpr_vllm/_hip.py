@@ -34,7 +34,7 @@ SIGNATURES: dict[str, list] = {
     "fxpr_float_to_fixed": [_P, _I, _P, _I, _I, _L, _P],
     "fxpr_fixed_to_float": [_P, _I, _P, _I, _I, _L, _P],
     "fxpr_fixed_row_sum": [_P, _I, _P, _I, _L, _L, _P],
-    "fxpr_rms_norm": [_P, _P, _P, _P, _I, _L, _L, _F, _I, _I, _P],
+    "fxpr_rms_norm": [_P, _P, _P, _P, _I, _L, _L, _F, _P],
     "fxpr_log_softmax": [_P, _I, _P, _I, _L, _L, _I, _I, _P],
     "fxpr_gemm": [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _P],
     "fxpr_gemm_splits": [_L, _L, _L, _I, _I],

@@ -55,9 +55,11 @@ def _as_2d(x: torch.Tensor) -> torch.Tensor:
     return x.reshape(-1, x.shape[-1])
 
 
-def _rms_launch(x, w, residual, eps, int_bits=None, frac_bits=None):
+def _rms_launch(x, w, residual, eps):
     """Validation and copy-back rules of the reference's _common_launch
-    (fxpr_vllm/_triton/rms_norm.py:78-134)."""
+    (fxpr_vllm/_triton/rms_norm.py:78-134). The sum of squares has its own
+    per-row block floating-point integer format (csrc/rows.hip), so, like the
+    reference's launcher, this takes no fixed-point knobs."""
     if not x.is_cuda or not w.is_cuda:
         raise RuntimeError("rms_norm: x and w must be CUDA")
     if x.dtype not in _SUPPORTED_DTYPES:
@@ -71,7 +73,6 @@ def _rms_launch(x, w, residual, eps, int_bits=None, frac_bits=None):
             raise TypeError("rms_norm: residual dtype must match input dtype")
         if residual.shape != x.shape:
             raise ValueError("rms_norm: residual shape must match x")
-    b, f = _bits(int_bits, frac_bits)
 
     x_2d = _as_2d(x).contiguous()
     y_2d = torch.empty_like(x_2d)
@@ -91,19 +92,21 @@ def _rms_launch(x, w, residual, eps, int_bits=None, frac_bits=None):
 
     _hip.call(
         "fxpr_rms_norm", x_2d.data_ptr(), _hip.ptr(r_storage), w_c.data_ptr(), y_2d.data_ptr(),
-        _hip.DTYPE_CODE[x.dtype], rows, hidden, float(eps), b, f, _hip.stream_ptr(x.device),
+        _hip.DTYPE_CODE[x.dtype], rows, hidden, float(eps), _hip.stream_ptr(x.device),
     )
     if residual is not None and r_storage.data_ptr() != residual.data_ptr():
         residual.copy_(r_storage.view_as(residual))
     return y_2d.view_as(x)
 
 
-def rms_norm_fxp_run(x, w, eps, int_bits=None, frac_bits=None):
-    return _rms_launch(x, w, None, eps, int_bits, frac_bits)
+def rms_norm_fxp_run(x, w, eps):
+    """fxpr_vllm/_triton/rms_norm.py:137-142."""
+    return _rms_launch(x, w, None, eps)
 
 
-def rms_norm_fxp_residual_run(x, residual, w, eps, int_bits=None, frac_bits=None):
-    return _rms_launch(x, w, residual, eps, int_bits, frac_bits)
+def rms_norm_fxp_residual_run(x, residual, w, eps):
+    """fxpr_vllm/_triton/rms_norm.py:145-151 (mutates residual)."""
+    return _rms_launch(x, w, residual, eps)
 
 
 def log_softmax_fxp_run(x, int_bits, frac_bits, out_dtype=None):
