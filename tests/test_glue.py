@@ -91,7 +91,7 @@ def test_register_registers_everything_once(vllm_stub):
     import vllm.model_executor.layers.layernorm as layernorm_mod
     from fxpr_vllm import register as reg
 
-    reg._registered = False
+    reg.reset_registration()
     reg.register()
     from fxpr_vllm.quantisation_config import FixedPointConfig
     from fxpr_vllm.rms_norm import DeterministicRMSNorm
@@ -116,9 +116,58 @@ def test_register_respects_disable_rms_norm(vllm_stub, monkeypatch):
     from fxpr_vllm import register as reg
 
     op_registry.clear()
-    reg._registered = False
+    reg.reset_registration()
     reg.register()
     assert "rms_norm" not in op_registry
+
+
+def test_backend_path_resolves_and_early_imports_are_named(vllm_stub, caplog):
+    import importlib
+    import logging
+    import types
+
+    import vllm.model_executor.layers.layernorm as layernorm_mod
+    from fxpr_vllm import monkey_patches
+
+    module, _, cls = monkey_patches.BACKEND_CLASS_PATH.rpartition(".")
+    from fxpr_vllm.attention_backend import DeterministicAttentionBackend
+
+    assert getattr(importlib.import_module(module), cls) is DeterministicAttentionBackend
+    # a model module that bound vLLM's RMSNorm before the hook keeps it and is named
+    early = types.ModuleType("vllm.model_executor.models.early_model")
+    early.RMSNorm = layernorm_mod.RMSNorm
+    sys.modules[early.__name__] = early
+    try:
+        with caplog.at_level(logging.WARNING, logger="fxpr_vllm"):
+            replaced = monkey_patches.install_rms_norm()
+        assert replaced is early.RMSNorm
+        assert any("early_model" in r.message for r in caplog.records)
+    finally:
+        del sys.modules[early.__name__]
+
+
+def test_register_retries_a_failed_step(vllm_stub, monkeypatch):
+    from vllm.model_executor.layers.quantization import QUANTIZATION_METHODS
+
+    from fxpr_vllm import monkey_patches
+    from fxpr_vllm import register as reg
+
+    reg.reset_registration()
+    calls = []
+
+    def flaky():
+        calls.append(1)
+        if len(calls) == 1:
+            raise RuntimeError("transient")
+        return monkey_patches.BACKEND_CLASS_PATH
+
+    monkeypatch.setattr(monkey_patches, "install_attention_backend", flaky)
+    with pytest.raises(RuntimeError):
+        reg.register()
+    assert "fixedpoint" in QUANTIZATION_METHODS   # the step before the failure stays done
+    QUANTIZATION_METHODS.clear()
+    reg.register()
+    assert len(calls) == 2 and not QUANTIZATION_METHODS
 
 
 @pytest.mark.parametrize("lm_head", [True, False])
@@ -301,3 +350,29 @@ def test_attention_impl_matches_ops(vllm_stub):
     assert bits_equal(out.view(T, Hq, D), ref)
     # profiling call without metadata: zeros
     assert torch.count_nonzero(impl.forward(None, q, k, v, kv, None)) == 0
+
+
+@pytest.mark.gpu
+def test_warmups_run_clean_once(caplog):
+    # the warm-ups swallow errors by design, so a broken launch would only
+    # show as a logged warning: require none, and a second call to do nothing
+    import logging
+
+    import fxpr_vllm  # noqa: F401
+    from fxpr_vllm import warmup
+
+    warmup._done.clear()
+    dev = torch.device("cuda")
+    w = _bf16(512, 384, seed=11, scale=0.05).cuda().t()
+    with caplog.at_level(logging.WARNING, logger="fxpr_vllm"):
+        for dtype in (torch.bfloat16, torch.float16):
+            warmup.warmup_attention(8, 2, 128, dtype, dev, 0, 0.0, 32, 16)
+        warmup.warmup_rms_norm(4096, torch.bfloat16, dev)
+        warmup.warmup_gemm(w, 32, 16)
+        warmup.warmup_gemm(w, 64, 16)
+    assert not [r for r in caplog.records if "warm-up" in r.message], caplog.text
+    n = len(warmup._done)
+    assert n == 5
+    warmup.warmup_gemm(w, 32, 16)
+    warmup.warmup_rms_norm(4096, torch.bfloat16, dev)
+    assert len(warmup._done) == n

@@ -1,23 +1,33 @@
-"""Process-wide knobs, read once from the environment.
+"""Process-wide settings of the fixed-point plugin, read from the environment.
 
-Same variables, defaults and fallbacks as the reference plugin
-(fxpr_vllm/config.py:11-73 of Gursukh/vLLM-Triton-Fixed-Point-Reductions):
+The variables, their accepted values and defaults are the reference plugin's
+(fxpr_vllm/config.py:6-73 of Gursukh/vLLM-Triton-Fixed-Point-Reductions), so
+a deployment configured for it behaves the same here:
 
-    FXPR_INT_BITS                  16 / 32 / 64 (default 32), else warn + default
-    FXPR_FRAC_BITS                 8 / 16 / 32 (default 16), else warn + default
-    FXPR_DISABLE_RMS_NORM=1        keep vLLM's stock RMSNorm
-    FXPR_DISABLE_LM_HEAD=1         keep vLLM's lm_head matmul
-    FXPR_DISABLE_ATTENTION_WARMUP=1, FXPR_DISABLE_GEMM_WARMUP=1,
-    FXPR_DISABLE_RMS_NORM_WARMUP=1 skip the load-time warm-up calls
+    variable                         accepted              default
+    FXPR_INT_BITS                    16 | 32 | 64          32
+    FXPR_FRAC_BITS                   8 | 16 | 32           16
+    FXPR_DISABLE_RMS_NORM            "1" = keep vLLM's RMSNorm
+    FXPR_DISABLE_LM_HEAD             "1" = keep vLLM's lm_head matmul
+    FXPR_DISABLE_ATTENTION_WARMUP    "1" = no attention warm-up at first use
+    FXPR_DISABLE_GEMM_WARMUP         "1" = no GEMM warm-up at weight load
+    FXPR_DISABLE_RMS_NORM_WARMUP     "1" = no RMSNorm warm-up at weight load
 
-RMSNorm and log-softmax take their fixed-point format from FXPR_INT_BITS /
-FXPR_FRAC_BITS, since their schemas carry no bit arguments.
+A value that does not parse or is not accepted is logged on the "fxpr_vllm"
+logger and replaced by the default: a mistyped knob must not keep a serving
+process from starting. The knobs set the fixed-point format of the GEMM,
+attention and log-softmax paths; RMSNorm has a format of its own.
+
+The settings are read on first use and cached for the life of the process
+(vLLM starts one process per GPU); reset_runtime_config() drops the cache.
 """
 
 from __future__ import annotations
 
+import functools
 import logging
 import os
+from collections.abc import Mapping
 from dataclasses import dataclass
 
 DEFAULT_FXP_INT_BITS = 32
@@ -26,23 +36,10 @@ DEFAULT_FXP_FRAC_BITS = 16
 logger = logging.getLogger("fxpr_vllm")
 
 
-def _read_int(name: str, default: int) -> int:
-    raw = os.environ.get(name)
-    if raw is None or raw == "":
-        return default
-    try:
-        return int(raw)
-    except ValueError:
-        logger.warning("Ignoring malformed %s=%r; using default %d", name, raw, default)
-        return default
-
-
-def _flag(name: str) -> bool:
-    return os.environ.get(name) == "1"
-
-
 @dataclass(frozen=True)
 class FxpRuntimeConfig:
+    """The resolved settings (field names are the reference's)."""
+
     fxp_int_bits: int = DEFAULT_FXP_INT_BITS
     fxp_frac_bits: int = DEFAULT_FXP_FRAC_BITS
     enable_rms_norm: bool = True
@@ -52,39 +49,61 @@ class FxpRuntimeConfig:
     disable_rms_norm_warmup: bool = False
 
 
-def load_runtime_config() -> FxpRuntimeConfig:
-    int_bits = _read_int("FXPR_INT_BITS", DEFAULT_FXP_INT_BITS)
-    if int_bits not in (16, 32, 64):
-        logger.warning("Invalid FXPR_INT_BITS=%d; must be 16/32/64. Using default %d.",
-                       int_bits, DEFAULT_FXP_INT_BITS)
-        int_bits = DEFAULT_FXP_INT_BITS
-    frac_bits = _read_int("FXPR_FRAC_BITS", DEFAULT_FXP_FRAC_BITS)
-    if frac_bits not in (8, 16, 32):
-        logger.warning("Invalid FXPR_FRAC_BITS=%d; must be 8/16/32. Using default %d.",
-                       frac_bits, DEFAULT_FXP_FRAC_BITS)
-        frac_bits = DEFAULT_FXP_FRAC_BITS
-    return FxpRuntimeConfig(
-        fxp_int_bits=int_bits,
-        fxp_frac_bits=frac_bits,
-        enable_rms_norm=not _flag("FXPR_DISABLE_RMS_NORM"),
-        enable_lm_head=not _flag("FXPR_DISABLE_LM_HEAD"),
-        disable_attention_warmup=_flag("FXPR_DISABLE_ATTENTION_WARMUP"),
-        disable_gemm_warmup=_flag("FXPR_DISABLE_GEMM_WARMUP"),
-        disable_rms_norm_warmup=_flag("FXPR_DISABLE_RMS_NORM_WARMUP"),
-    )
+@dataclass(frozen=True)
+class _IntChoice:
+    """An integer knob restricted to a fixed set of values."""
+
+    var: str
+    accepted: tuple[int, ...]
+    default: int
+
+    def resolve(self, environ: Mapping[str, str]) -> int:
+        text = environ.get(self.var, "").strip()
+        if not text:
+            return self.default
+        try:
+            value = int(text, 10)
+        except ValueError:
+            value = None
+        if value in self.accepted:
+            return value
+        logger.warning("%s=%r is not one of %s; falling back to %d", self.var, text,
+                       "/".join(str(v) for v in self.accepted), self.default)
+        return self.default
 
 
-_runtime_config: FxpRuntimeConfig | None = None
+_CHOICES = {
+    "fxp_int_bits": _IntChoice("FXPR_INT_BITS", (16, 32, 64), DEFAULT_FXP_INT_BITS),
+    "fxp_frac_bits": _IntChoice("FXPR_FRAC_BITS", (8, 16, 32), DEFAULT_FXP_FRAC_BITS),
+}
+
+# field -> variable whose value "1" flips the field away from its default
+_SWITCHES = {
+    "enable_rms_norm": "FXPR_DISABLE_RMS_NORM",
+    "enable_lm_head": "FXPR_DISABLE_LM_HEAD",
+    "disable_attention_warmup": "FXPR_DISABLE_ATTENTION_WARMUP",
+    "disable_gemm_warmup": "FXPR_DISABLE_GEMM_WARMUP",
+    "disable_rms_norm_warmup": "FXPR_DISABLE_RMS_NORM_WARMUP",
+}
 
 
+def load_runtime_config(environ: Mapping[str, str] | None = None) -> FxpRuntimeConfig:
+    """Resolve every knob from `environ` (default: the process environment)."""
+    env = os.environ if environ is None else environ
+    defaults = FxpRuntimeConfig()
+    fields: dict[str, object] = {name: c.resolve(env) for name, c in _CHOICES.items()}
+    for name, var in _SWITCHES.items():
+        flipped = env.get(var, "").strip() == "1"
+        fields[name] = (not getattr(defaults, name)) if flipped else getattr(defaults, name)
+    return FxpRuntimeConfig(**fields)
+
+
+@functools.lru_cache(maxsize=1)
 def get_runtime_config() -> FxpRuntimeConfig:
-    global _runtime_config
-    if _runtime_config is None:
-        _runtime_config = load_runtime_config()
-    return _runtime_config
+    """The process's settings, resolved once."""
+    return load_runtime_config()
 
 
 def reset_runtime_config() -> None:
-    """Forget the cached config so the next call re-reads the environment."""
-    global _runtime_config
-    _runtime_config = None
+    """Drop the cached settings; the next get_runtime_config() re-reads the environment."""
+    get_runtime_config.cache_clear()

@@ -1,42 +1,58 @@
-"""vLLM plugin entry point (``vllm.general_plugins`` -> fxpr_vllm.register:register).
+"""vLLM plugin entry point (``vllm.general_plugins``: fxpr_vllm.register:register).
 
-Same effects as the reference (fxpr_vllm/register.py:12-40): registers the
-"fixedpoint" quantization config, the CUSTOM attention backend and, unless
-FXPR_DISABLE_RMS_NORM=1, the fixed-point RMSNorm. Idempotent: vLLM calls
-plugins in every process it starts.
+vLLM runs every general plugin in each process it starts, so register() may
+run many times per process. It performs the reference plugin's three hooks
+(fxpr_vllm/register.py:12-40 of Gursukh/vLLM-Triton-Fixed-Point-Reductions):
+the "fixedpoint" quantization config, the CUSTOM attention backend and,
+unless FXPR_DISABLE_RMS_NORM=1, the fixed-point RMSNorm. Each hook is a named
+step that runs at most once per process; a step that raises is not recorded,
+so a later call retries it.
 """
 
 from __future__ import annotations
 
 import logging
+from collections.abc import Callable, Iterator
 
-from .config import get_runtime_config
+from .config import FxpRuntimeConfig, get_runtime_config
 
 logger = logging.getLogger("fxpr_vllm")
 
-_registered = False
+_completed: set[str] = set()
+
+
+def _install_quant_config() -> None:
+    from vllm.model_executor.layers.quantization import register_quantization_config
+
+    from .quantisation_config import FixedPointConfig
+
+    register_quantization_config(FixedPointConfig.get_name())(FixedPointConfig)
+
+
+def _steps(cfg: FxpRuntimeConfig) -> Iterator[tuple[str, Callable[[], object]]]:
+    from . import monkey_patches
+
+    yield "quantization config 'fixedpoint'", _install_quant_config
+    yield "attention backend CUSTOM", monkey_patches.install_attention_backend
+    if cfg.enable_rms_norm:
+        yield "RMSNorm", monkey_patches.install_rms_norm
 
 
 def register() -> None:
-    global _registered
-    if _registered:
-        return
+    """Install every enabled hook that has not run in this process yet."""
     cfg = get_runtime_config()
-    logger.info("fxpr_vllm: int_bits=%d frac_bits=%d rms_norm=%s lm_head=%s", cfg.fxp_int_bits,
-                cfg.fxp_frac_bits, cfg.enable_rms_norm, cfg.enable_lm_head)
+    pending = [(label, step) for label, step in _steps(cfg) if label not in _completed]
+    if not pending:
+        return
+    for label, step in pending:
+        step()
+        _completed.add(label)
+        logger.info("fxpr_vllm: installed %s", label)
+    logger.info("fxpr_vllm: Q%d in int%d accumulators; RMSNorm %s, lm_head through gemm_fxp %s",
+                cfg.fxp_frac_bits, cfg.fxp_int_bits, "on" if cfg.enable_rms_norm else "off",
+                "on" if cfg.enable_lm_head else "off")
 
-    from vllm.model_executor.layers.quantization import register_quantization_config
 
-    from . import monkey_patches
-    from .quantisation_config import FixedPointConfig
-
-    register_quantization_config("fixedpoint")(FixedPointConfig)
-    logger.info("registered fixedpoint quant config")
-    monkey_patches.patch_attention_backend()
-    logger.info("registered CUSTOM attention backend")
-    if cfg.enable_rms_norm:
-        monkey_patches.patch_rms_norm()
-        logger.info("patched RMSNorm")
-    if cfg.enable_lm_head:
-        logger.info("lm_head matmul will route through gemm_fxp")
-    _registered = True
+def reset_registration() -> None:
+    """Forget which hooks ran (tests re-register against a fresh vLLM)."""
+    _completed.clear()
