@@ -57,3 +57,30 @@ def seeded(shape, seed: int, std: float = 1.0, mean: float = 0.0, dtype=torch.fl
     """Seeded CPU normal data (the bench and tests generate on the CPU, then copy)."""
     g = torch.Generator("cpu").manual_seed(seed)
     return (torch.randn(shape, generator=g, dtype=torch.float32) * std + mean).to(dtype)
+
+
+def close_report(got: torch.Tensor, want: torch.Tensor, rtol: float = 1e-2, atol_rms: float = 1e-3) -> str:
+    """'' when every element satisfies |got - want| <= rtol * |want| + atol,
+    with atol = atol_rms * RMS(want) (a floor for outputs near zero, where a
+    relative bound means nothing); else a description of the worst element.
+
+    rtol = 1e-2 is the north star's "within 1e-2 relative" for the GEMM and
+    attention paths. Non-finite values must match exactly."""
+    g = got.detach().cpu().double().reshape(-1)
+    w = want.detach().cpu().double().reshape(-1)
+    if g.shape != w.shape:
+        return f"shape {tuple(got.shape)} != {tuple(want.shape)}"
+    fin = torch.isfinite(w)
+    same_nonfinite = (torch.isnan(g) & torch.isnan(w)) | (g == w)
+    if not bool(torch.all(fin | same_nonfinite)):
+        return "non-finite values differ"
+    g, w = g[fin], w[fin]
+    if w.numel() == 0:
+        return ""
+    atol = atol_rms * float(torch.sqrt((w * w).mean()))
+    excess = (g - w).abs() - (rtol * w.abs() + atol)
+    i = int(torch.argmax(excess))
+    if excess[i] <= 0:
+        return ""
+    return (f"{int((excess > 0).sum())} elements out of tolerance; worst: got {g[i].item()!r} want "
+            f"{w[i].item()!r} (rtol {rtol}, atol {atol:.3g})")

@@ -19,7 +19,7 @@ import torch
 
 import fxpr_vllm  # noqa: F401
 from oracle import attention as A
-from tests._util import IO_NAME, from_np, to_np
+from tests._util import IO_NAME, close_report, from_np, to_np
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -85,8 +85,16 @@ def prefill_case(seq_lens, hq, hkv, d, dtype, seed=42, scale=1.0):
 
 
 def close(got, want, tol=1e-2):
-    g, w = got.double().cpu(), want.double().cpu()
-    return (g - w).abs().max().item() <= tol * max(1.0, w.abs().max().item())
+    """Per element |got - want| <= tol * |want| + 1e-2 * RMS(want).
+
+    The floor covers outputs near zero: every weight P is rounded to the I/O
+    type before the weighted-V product (the reference's IO(w),
+    fxpr_vllm/_triton/attention.py:287), so two orders of the same softmax
+    (512-key chunk maxima vs one maximum per row, or NVIDIA vs MFMA) differ by
+    bf16 rounding noise of about 2^-9 * RMS(V) / sqrt(keys) per element."""
+    report = close_report(got, want, rtol=tol, atol_rms=1e-2)
+    assert not report, report
+    return True
 
 
 # --------------------------------------------------------------------------
@@ -312,14 +320,18 @@ def test_config4_decode_full_shape_properties():
     ref = attend(q, kv, qsl, sl_d, bt_d, 1, 1)
     for s in (2, 4, 8, 16, 0):
         assert torch.equal(attend(q, kv, qsl, sl_d, bt_d, 1, s), ref), s
-    for r in (0, 17, 63):
+    longest = int(torch.argmax(sl))
+    for r in (0, 17, longest):
         nblk = (int(sl[r]) + ps - 1) // ps
         blocks = bt[r, :nblk].long()
         sub_kv = kv[blocks.to(DEV)].cpu()
         sub_bt = torch.arange(nblk, dtype=torch.int32).reshape(1, nblk)
-        want = oracle(q[r:r + 1].cpu(), sub_kv, torch.tensor([0, 1], dtype=torch.int32),
-                      sl[r:r + 1], sub_bt)
-        assert close(ref[r:r + 1], want)
+        sub = (q[r:r + 1].cpu(), sub_kv, torch.tensor([0, 1], dtype=torch.int32), sl[r:r + 1], sub_bt)
+        # the kernels' algorithm (512-key chunks) and the reference's (one
+        # maximum per row), up to the longest context (16 chunks)
+        assert close(ref[r:r + 1], oracle(*sub))
+        assert close(ref[r:r + 1], oracle(*sub, chunk_keys=None))
+    assert int(sl[longest]) > 7680  # 16 chunks of 512 keys
 
 
 # --------------------------------------------------------------------------

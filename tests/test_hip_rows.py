@@ -369,3 +369,29 @@ def test_rms_norm_rrms_correctly_rounded():
     y = K.rms_norm_fxp_run(x.to(DEV), w.to(DEV), 1e-6).cpu()
     want = torch.from_numpy(R.rms_norm(x.numpy(), w.numpy(), 1e-6, "f32")[0])
     assert torch.equal(y, want), mismatch_report(y, want)
+
+
+@pytest.mark.parametrize("b", [32, 64])
+def test_config1_plumbing_full_shape(b):
+    # fp32 x [4096, 4096] ~ N(0,1), residual ~ N(0,1),
+    # weight ~ N(1, 0.1), eps 1e-6, seed 0; float_to_fixed -> fixed_row_sum ->
+    # fixed_to_float at Q16.16 in int32 / int64, and RMSNorm (+ residual),
+    # all bit for bit against the oracle
+    g = torch.Generator("cpu").manual_seed(0)
+    x = torch.randn(4096, 4096, generator=g)
+    r = torch.randn(4096, 4096, generator=g)
+    w = torch.randn(4096, generator=g) * 0.1 + 1.0
+    xd = x.to(DEV)
+    q = torch.ops.fxpr.float_to_fixed(xd, b, 16)
+    s = torch.ops.fxpr.fixed_row_sum(q, b)
+    y = torch.ops.fxpr.fixed_to_float(s, 32, 16)
+    q_want = N.float_to_fixed(x.numpy(), b, 16)
+    assert np.array_equal(q.cpu().numpy(), q_want)
+    s_want = N.fixed_row_sum(q_want, b)
+    assert np.array_equal(s.cpu().numpy(), s_want)
+    assert np.array_equal(y.cpu().numpy(), N.fixed_to_float(s_want, 32, 16))
+    if b == 32:
+        y, _ = _rms_check(x, w, None)
+        _rms_check(x, w, r)
+        ref = x.double() * w.double() / torch.sqrt((x.double() ** 2).mean(-1, keepdim=True) + 1e-6)
+        assert torch.allclose(y.cpu().double(), ref, atol=5e-4, rtol=5e-4)
