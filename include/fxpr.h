@@ -117,6 +117,26 @@ int fxpr_log_softmax(const void* x, int x_dtype, void* y, int y_dtype,
                      void* stream);
 
 /*
+ * Deterministic greedy sampling with log-probabilities over contiguous
+ * [rows, cols] logits (f32, f16 or bf16), cols < 2^31. Each row's order is
+ * largest value first, equal values by ascending index, every NaN above +inf,
+ * -0 equal to +0. sampled[r] (int64) is the first element of the order and
+ * sampled_logprob[r] (fp32) its log-probability; with num_logprobs = k in
+ * [1, min(64, cols)], topk_ids / topk_logprobs [rows, k] hold the first k
+ * elements of the order and their log-probabilities (both may be NULL for
+ * k = 0). A log-probability is fl32(x_j) - lse with lse computed exactly as in
+ * fxpr_log_softmax(int_bits, frac_bits): the values equal that function's
+ * fp32 outputs bit for bit.
+ * No counterpart exists in the reference: it lists fxpr_vllm/sampling.py
+ * (README.md:69) but does not ship it; this is the step after the lm_head
+ * GEMM and log_softmax_fxp.
+ */
+int fxpr_sample_greedy(const void* logits, int x_dtype, int64_t rows,
+                       int64_t cols, int num_logprobs, int int_bits,
+                       int frac_bits, int64_t* sampled, float* sampled_logprob,
+                       int64_t* topk_ids, float* topk_logprobs, void* stream);
+
+/*
  * Fixed-point GEMM, C[M,N] = IO(fl32(acc) * 2^-frac_bits (+ bias)) with
  * acc = wrapping int_bits sum over K-tiles t (128 wide for bf16/f16, 64 for
  * f32; zero-padded tail) of RNE_sat(fp32 dot(A[m, t], B[t, n]) * 2^f).

@@ -231,3 +231,8 @@ def test_first_launch_inside_capture_fresh_process(tmp_path):
     res = subprocess.run([sys.executable, str(script)], capture_output=True, text=True, timeout=180)
     assert res.returncode == 0, res.stdout + res.stderr
     assert "first-launch capture ok" in res.stdout
+
+
+def test_capture_sample_greedy():
+    check_capture(lambda s: {"x": _randn((16, 128256), 160 + s, scale=4.0)},
+                  lambda t: torch.ops.fxpr.sample_greedy_fxp(t["x"], 20, 32, 16))

@@ -1,0 +1,114 @@
+"""GPU parity: the greedy sampler (sample_greedy_fxp, DeterministicSampler).
+
+Token ids and top-k ids equal the oracle's order exactly, log-probabilities
+equal the oracle's and log_softmax_fxp's fp32 outputs bit for bit, at full
+vocabulary and on tie-heavy, NaN, infinite and ragged rows; tokens equal
+torch.argmax on finite rows; rows do not depend on the batch.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import fxpr_vllm  # noqa: F401
+from fxpr_vllm._kernels import sampling as KS
+from fxpr_vllm.sampling import DeterministicSampler
+from oracle import sampling as S
+from tests._util import IO_NAME, to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _logits(rows, vocab, seed, dtype=torch.bfloat16, ties=False):
+    g = torch.Generator("cpu").manual_seed(seed)
+    x = torch.randn(rows, vocab, generator=g) * 4.0
+    if ties:
+        x = torch.round(x)
+    return x.to(dtype)
+
+
+def _same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    """Bitwise equal fp32, any NaN matching any NaN (the host's default NaN
+    carries the sign bit, the GPU's does not)."""
+    return a.shape == b.shape and bool(np.all((a.view(np.uint32) == b.view(np.uint32)) |
+                                              (np.isnan(a) & np.isnan(b))))
+
+
+def _check(x, k, b, f):
+    got = KS.sample_greedy_fxp_run(x.to(DEV), k, b, f)
+    ids, lp, top, top_lp = S.sample_greedy(to_np(x), IO_NAME[x.dtype], k, b, f)
+    assert np.array_equal(got[0].cpu().numpy(), ids)
+    assert _same_bits(got[1].cpu().numpy(), lp)
+    assert np.array_equal(got[2].cpu().numpy(), top)
+    assert _same_bits(got[3].cpu().numpy(), top_lp)
+    return got
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("k", [0, 1, 20, 64])
+def test_full_vocab_bit_exact(dtype, k):
+    _check(_logits(8, 128_256, seed=k, dtype=dtype), k, 32, 16)
+
+
+@pytest.mark.parametrize("b,f", [(32, 16), (64, 32), (16, 8), (64, 63)])
+@pytest.mark.parametrize("shape", [(3, 1), (5, 7), (4, 1001), (2, 300_001)])
+def test_formats_and_ragged_rows(b, f, shape):
+    _check(_logits(*shape, seed=sum(shape), ties=True), min(5, shape[1]), b, f)
+
+
+def test_special_rows():
+    V = 4096
+    x = torch.round(torch.randn(6, V, generator=torch.Generator("cpu").manual_seed(3)) * 2)
+    x[1, 100] = float("nan")
+    x[1, 3000] = float("nan")
+    x[2] = 0.0
+    x[2, ::2] = -0.0
+    x[3, 5] = float("inf")
+    x[3, 6] = float("inf")
+    x[4] = -float("inf")
+    x[5, :] = 7.0
+    for dtype in (torch.float32, torch.bfloat16):
+        ids = _check(x.to(dtype), 10, 32, 16)[0].cpu()
+        assert ids.tolist()[1:] == [100, 0, 5, 0, 0]
+
+
+def test_logprobs_equal_log_softmax_and_tokens_equal_argmax():
+    x = _logits(32, 128_256, seed=11).to(DEV)
+    ids, lp, top, top_lp = torch.ops.fxpr.sample_greedy_fxp(x, 20, 32, 16)
+    full = torch.ops.fxpr.log_softmax_fxp(x, 32, 16, torch.float32)
+    assert torch.equal(ids, torch.argmax(x, dim=-1))
+    assert torch.equal(lp.view(torch.int32), full.gather(1, ids[:, None])[:, 0].view(torch.int32))
+    assert torch.equal(top_lp.view(torch.int32), full.gather(1, top).view(torch.int32))
+    assert torch.all(top_lp[:, :-1] >= top_lp[:, 1:])
+
+
+def test_batch_invariance_and_module():
+    x = _logits(64, 32_000, seed=5).to(DEV)
+    full = torch.ops.fxpr.sample_greedy_fxp(x, 8, 32, 16)
+    for r in (0, 17, 63):
+        one = torch.ops.fxpr.sample_greedy_fxp(x[r:r + 1].clone(), 8, 32, 16)
+        for a, b in zip(one, full):
+            assert torch.equal(a[0], b[r])
+    out = DeterministicSampler()(x.view(4, 16, 32_000), num_logprobs=3)
+    assert out.token_ids.shape == (4, 16) and out.topk_logprobs.shape == (4, 16, 3)
+    assert torch.equal(out.token_ids.reshape(-1), full[0])
+    assert torch.equal(out.topk_token_ids.reshape(64, 3), full[2][:, :3])
+    lps = DeterministicSampler.compute_logprobs(x)
+    assert torch.equal(lps.gather(1, full[0][:, None])[:, 0], full[1])
+
+
+def test_errors():
+    x = _logits(2, 100, seed=0).to(DEV)
+    with pytest.raises(ValueError):
+        torch.ops.fxpr.sample_greedy_fxp(x, 65, 32, 16)
+    with pytest.raises(ValueError):
+        torch.ops.fxpr.sample_greedy_fxp(x[:, :3], 4, 32, 16)
+    with pytest.raises(ValueError):
+        torch.ops.fxpr.sample_greedy_fxp(x, 2, 32, 12)
+    with pytest.raises(TypeError):
+        torch.ops.fxpr.sample_greedy_fxp(x.double(), 2, 32, 16)
+    e = torch.ops.fxpr.sample_greedy_fxp(x[:0], 2, 32, 16)
+    assert e[0].shape == (0,) and e[2].shape == (0, 2)

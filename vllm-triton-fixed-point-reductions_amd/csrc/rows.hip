@@ -10,90 +10,12 @@
 // in registers between the reduction pass and the output pass so x is read
 // from HBM once.
 
-#include <cmath>
-#include <type_traits>
-
-#include "fxp_device.h"
-#include "fxpr_internal.h"
+#include "rows_impl.h"
 
 namespace fxpr {
 namespace {
 
-// N consecutive elements. For N > 1 a native vector, so arrays of them stay
-// in registers (a struct holding a plain array is copied with memcpys that
-// keep such arrays in scratch memory).
-template <typename T, int N, bool = (N > 1)> struct VecImpl { T v[N]; };
-template <typename T, int N> struct alignas(sizeof(T) * N) VecImpl<T, N, true> {
-  typedef T VT __attribute__((ext_vector_type(N)));
-  VT v;
-};
-template <typename T, int N> using Vec = VecImpl<T, N>;
-
-constexpr int kMaxThreads = 1024;
-
-__device__ __forceinline__ float max_nan(float a, float b) {
-  return (a != a || a > b) ? a : b;  // NaN wins, otherwise the larger value
-}
-
-__device__ float block_max(float v, float* smem) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max_nan(v, __shfl_xor(v, o, 64));
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();
-  if (lane == 0) smem[wave] = v;
-  __syncthreads();
-  float r = smem[0];
-  for (int w = 1; w < nw; ++w) r = max_nan(r, smem[w]);
-  return r;
-}
-
-using u128 = unsigned __int128;
-
-__device__ __forceinline__ u128 shfl_xor_u128(u128 v, int o) {
-  uint64_t lo = static_cast<uint64_t>(v), hi = static_cast<uint64_t>(v >> 64);
-  lo = __shfl_xor(lo, o, 64);
-  hi = __shfl_xor(hi, o, 64);
-  return (static_cast<u128>(hi) << 64) | lo;
-}
-
-// Exact workgroup sum of unsigned 64- or 128-bit lane values.
-template <class U> __device__ U block_exact_sum(U v, U* smem) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    if constexpr (sizeof(U) == 16) v += shfl_xor_u128(v, o);
-    else v += __shfl_xor(v, o, 64);
-  }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();
-  if (lane == 0) smem[wave] = v;
-  __syncthreads();
-  U r = smem[0];
-  for (int w = 1; w < nw; ++w) r += smem[w];
-  return r;
-}
-
-__device__ __forceinline__ uint32_t cvt_sat_u32(float integral) {
-  // v_cvt_u32_f32 saturates to [0, 2^32 - 1] and maps NaN to 0
-  uint32_t o;
-  asm("v_cvt_u32_f32 %0, %1" : "=v"(o) : "v"(integral));
-  return o;
-}
-
-template <int BITS> __device__ __forceinline__ uint64_t quant_nonneg(float s) {
-  // s >= 0 or NaN, so the result is in [0, qmax]
-  if constexpr (BITS == 64) {
-    // RNE, then split r = h 2^32 + l exactly (r integral, h = floor(r 2^-32));
-    // branch-free, so arrays of row values around it stay in registers.
-    // NaN -> 0; r >= 2^63 -> qmax.
-    const float r = __builtin_rintf(s);
-    const float h = __builtin_floorf(__fmul_rn(r, 2.3283064365386963e-10f));
-    const float l = __fsub_rn(r, __fmul_rn(h, 4294967296.0f));
-    const uint64_t v = (static_cast<uint64_t>(cvt_sat_u32(h)) << 32) | cvt_sat_u32(l);
-    return v > 0x7fffffffffffffffull ? 0x7fffffffffffffffull : v;
-  } else {
-    return static_cast<uint64_t>(quant<BITS>(s));
-  }
-}
+using namespace rowk;
 
 // ---------------------------------------------------------------------------
 // Exact integer row sum, saturated once to OBITS.
@@ -326,14 +248,6 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(
   }
 }
 
-inline int threads_for(int64_t nchunks, int per_thread, int max_threads = kMaxThreads) {
-  int64_t t = cdiv(nchunks, per_thread);
-  t = cdiv(t, 64) * 64;
-  if (t < 64) t = 64;
-  if (t > max_threads) t = max_threads;
-  return static_cast<int>(t);
-}
-
 template <int DT, int VEC>
 int launch_rms_vec(const void* x, void* r, const void* w, void* y, int64_t rows, int64_t hidden,
                    float eps, hipStream_t st) {
@@ -375,55 +289,16 @@ int launch_rms(const void* x, void* r, const void* w, void* y, int64_t rows, int
 // gives -inf).
 // Pass 3: y_j = OUT(fl32(x_j) - lse).
 
-// Log-softmax workgroups are at most 512 threads (two waves per SIMD), so a
-// thread may hold 256 registers: a 128256-wide bf16 row stays in registers
-// (32 x 16 bytes per thread) next to the exp / log temporaries, unspilled.
-constexpr int kLsmThreads = 512;
-
-// quant_nonneg(exp_scaled_to_round(d, f)) by the rounding constant, for
-// 1.4143 * 2^f < 2^22 and <= qmax: the scaled value s = p * 2^(k+f) is exact
-// (p = 2^r for |r| <= 1/2 is in [0.7071, 1.4143], and k + f >= -116, so 2^(k+f)
-// is a normal fp32), fl(s + 1.5 * 2^23) is RNE(s) + 1.5 * 2^23 (the sum lies in
-// [2^23, 2^24), spacing 1; the constant is even), no saturation occurs, and
-// NaN d was raised to the floor as in exp_scaled_to_round. Returns the sum's
-// bit pattern, i.e. the quantised value + 0x4B400000.
-__device__ __forceinline__ uint32_t exp_scaled_rc_bits(float d, int f) {
-  d = fmaxf(d, FXPR_EXP_FLOOR);  // maxNum: NaN -> the floor
-  const float t = __fmul_rn(d, FXPR_LOG2E);
-  const float k = __builtin_rintf(t);
-  const float r = __fsub_rn(t, k);
-  const float s2 = __uint_as_float(static_cast<uint32_t>(static_cast<int>(k) + f + 127) << 23);
-  return __float_as_uint(__builtin_fmaf(exp2_poly(r), s2, 12582912.0f));
-}
-
-// fl32(v), round half to even, for an unsigned 64- or 128-bit integer. A
-// 128-bit value beyond 64 bits is shifted into 64 bits with the dropped bits
-// ORed into bit 0 (they lie far below the 24-bit rounding position, so only a
-// tie can depend on them), converted, and scaled back exactly.
-__device__ __forceinline__ float uint_to_f32(uint64_t v) { return static_cast<float>(v); }
-__device__ __forceinline__ float uint_to_f32(u128 v) {
-  const uint64_t hi = static_cast<uint64_t>(v >> 64);
-  if (hi == 0) return static_cast<float>(static_cast<uint64_t>(v));
-  const int n = 64 - __builtin_clzll(hi);
-  const u128 dropped = v & ((static_cast<u128>(1) << n) - 1);
-  const uint64_t top = static_cast<uint64_t>(v >> n) | (dropped != 0 ? 1u : 0u);
-  return __builtin_ldexpf(static_cast<float>(top), n);
-}
-
-// The per-lane sums of the rounding-constant path are plain 32-bit adds: the
-// host enables it only when elements per lane x the largest term stay below
-// 2^32. WIDE (64-bit terms only) takes 128-bit sums.
+// One workgroup per row: row_lse, then y_j = OUT(fl32(x_j) - lse) from the
+// chunks kept in registers (later chunks re-read).
 template <int XDT, int YDT, int VEC, int NREG, int BITS, bool WIDE>
 __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
     const typename Io<XDT>::T* __restrict__ x, typename Io<YDT>::T* __restrict__ y, int64_t cols,
     int frac, float inv_scale, int fast_sum) {
-  using XT = typename Io<XDT>::T;
-  using YT = typename Io<YDT>::T;
-  using XV = Vec<XT, VEC>;
-  using YV = Vec<YT, VEC>;
-  using SumT = typename std::conditional<WIDE, u128, uint64_t>::type;
+  using XV = Vec<typename Io<XDT>::T, VEC>;
+  using YV = Vec<typename Io<YDT>::T, VEC>;
   __shared__ float fred[kLsmThreads / 64];
-  __shared__ SumT ired[kLsmThreads / 64];
+  __shared__ LseSum<WIDE> ired[kLsmThreads / 64];
 
   const int64_t row = blockIdx.x;
   const int64_t nchunks = cols / VEC;
@@ -433,67 +308,7 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
   YV* yr = reinterpret_cast<YV*>(y + row * cols);
 
   XV keep[NREG];
-  // IEEE maximum (NaN propagates; gfx950's v_maximum3_f32): the same value
-  // as max_nan up to the sign of a zero maximum, which no output depends on
-  // (x - m and m + ln S come out the same for either zero).
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int i = 0; i < NREG; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * nthr;
-    if (c < nchunks) {
-      keep[i] = xr[c];
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) m = __builtin_elementwise_maximum(m, Io<XDT>::load(keep[i].v[j]));
-    }
-  }
-  for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) {
-    XV xv = xr[c];
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) m = __builtin_elementwise_maximum(m, Io<XDT>::load(xv.v[j]));
-  }
-  m = block_max(m, fred);
-
-  SumT acc = 0;
-  auto accum = [&](const XV& xv) {
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
-      acc += static_cast<SumT>(quant_nonneg<BITS>(exp_scaled_to_round(d, frac)));
-    }
-  };
-  if (BITS != 64 && fast_sum) {
-    uint32_t acc32 = 0;
-    auto accum_rc = [&](const XV& xv) {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j)
-        acc32 += exp_scaled_rc_bits(__fsub_rn(Io<XDT>::load(xv.v[j]), m), frac) - 0x4B400000u;
-    };
-#pragma unroll
-    for (int i = 0; i < NREG; ++i) {
-      const int64_t c = tid + static_cast<int64_t>(i) * nthr;
-      if (c < nchunks) accum_rc(keep[i]);
-    }
-    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum_rc(xr[c]);
-    acc = acc32;
-  } else {
-#pragma unroll
-    for (int i = 0; i < NREG; ++i) {
-      const int64_t c = tid + static_cast<int64_t>(i) * nthr;
-      if (c < nchunks) accum(keep[i]);
-    }
-    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum(xr[c]);
-  }
-  // The row stays in registers in its storage type: an empty asm "changing"
-  // it keeps the compiler from holding every element's fp32 widening (twice
-  // the registers) from the sum until the output pass.
-  if constexpr (VEC > 1) {
-#pragma unroll
-    for (int i = 0; i < NREG; ++i) asm volatile("" : "+v"(keep[i].v));
-  }
-  const SumT total = block_exact_sum(acc, ired);
-
-  const float lnS = total == 0 ? -__builtin_inff() : log_own(__fmul_rn(uint_to_f32(total), inv_scale));
-  const float lse = __fadd_rn(m, lnS);
+  const float lse = row_lse<XDT, VEC, NREG, BITS, WIDE>(xr, keep, nchunks, frac, inv_scale, fast_sum, fred, ired);
 
   auto emit = [&](int64_t c, const XV& xv) {
     YV yv;
@@ -515,29 +330,20 @@ int launch_lsm_vec(const void* x, void* y, int64_t rows, int64_t cols, int bits,
   using XT = typename Io<XDT>::T;
   using YT = typename Io<YDT>::T;
   constexpr int NREG = VEC == 1 ? 8 : 32;
-  const int64_t nchunks = cols / VEC;
-  const int nthr = threads_for(nchunks, NREG, kLsmThreads);
+  const LseShape sh = lse_shape(cols, VEC, NREG, bits, frac);
   const float inv = pow2f(-frac);
-  const double qmax = double(qmax_for_bits(bits));
-  // the largest term: e^0 * 2^f, with margin for the polynomial, or qmax
-  const double term_max = std::fmin(1.4143 * std::ldexp(1.0, frac) + 1.0, qmax);
-  // rounding-constant sums: 1.4143 * 2^f below 2^22 and qmax, and a lane's
-  // terms summing below 2^32
-  const double lane_elems = double(cdiv(nchunks, nthr)) * VEC;
-  const int fast = bits != 64 && term_max < 4194304.0 && term_max < qmax &&
-                   lane_elems * term_max < 4294967296.0;
-  const bool wide = double(cols) * term_max >= 18446744073709551616.0;
   dim3 grid(static_cast<unsigned>(rows));
   const XT* xp = static_cast<const XT*>(x);
   YT* yp = static_cast<YT*>(y);
+  const int n = sh.threads;
   if (bits == 16)
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 16, false><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, fast);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 16, false><<<grid, n, 0, st>>>(xp, yp, cols, frac, inv, sh.fast_sum);
   else if (bits == 32)
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 32, false><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, fast);
-  else if (!wide)
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 64, false><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, 0);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 32, false><<<grid, n, 0, st>>>(xp, yp, cols, frac, inv, sh.fast_sum);
+  else if (!sh.wide)
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 64, false><<<grid, n, 0, st>>>(xp, yp, cols, frac, inv, 0);
   else
-    log_softmax_kernel<XDT, YDT, VEC, NREG, 64, true><<<grid, nthr, 0, st>>>(xp, yp, cols, frac, inv, 0);
+    log_softmax_kernel<XDT, YDT, VEC, NREG, 64, true><<<grid, n, 0, st>>>(xp, yp, cols, frac, inv, 0);
   return launch_status();
 }
 

@@ -2,11 +2,13 @@
 
 The six reference schemas are kept verbatim (fxpr_vllm/_lib.py:13-33 of the
 reference) so callers and torch.compile graphs are a drop-in; PyTorch-ROCm
-dispatches HIP tensors through the CUDA key. Three schemas are new in this
+dispatches HIP tensors through the CUDA key. Four schemas are new in this
 build: fixed_row_sum (the integer sum the reference's tests do with torch,
 _tests/test_sum.py:12-16), log_softmax_fxp (listed in the reference
-README.md:60 but not shipped) and reshape_and_cache (the KV-cache write the
-reference backend takes from vLLM, attention_backend.py:253-277). Validation and error classes follow the
+README.md:60 but not shipped), sample_greedy_fxp (the sampler of the
+reference's README.md:69, likewise not shipped) and reshape_and_cache (the
+KV-cache write the reference backend takes from vLLM,
+attention_backend.py:253-277). Validation and error classes follow the
 reference impls (_lib.py:36-129).
 """
 
@@ -19,12 +21,13 @@ from ._kernels import cache as _cache
 from ._kernels import casts as _casts
 from ._kernels import gemm as _gemm
 from ._kernels import rows as _rows
+from ._kernels import sampling as _sampling
 
 _lib = torch.library.Library("fxpr", "DEF")
 
 _lib.define("float_to_fixed(Tensor x, int int_bits, int fxp_frac_bits) -> Tensor")
 _lib.define("fixed_to_float(Tensor x, int float_bits, int fxp_frac_bits) -> Tensor")
-# RMSNorm takes its fixed-point format from FXPR_INT_BITS / FXPR_FRAC_BITS.
+# RMSNorm's integer sum of squares has a per-row format of its own (no knobs).
 _lib.define("rms_norm_fxp(Tensor x, Tensor weight_fp32, float eps) -> Tensor")
 _lib.define(
     "rms_norm_fxp_residual(Tensor x, Tensor(a!) residual, Tensor weight_fp32, "
@@ -49,6 +52,10 @@ _lib.define(
 _lib.define(
     "reshape_and_cache(Tensor key, Tensor value, Tensor(a!) kv_cache, "
     "Tensor slot_mapping) -> ()"
+)
+_lib.define(
+    "sample_greedy_fxp(Tensor logits, int num_logprobs, int fxp_int_bits, "
+    "int fxp_frac_bits) -> (Tensor, Tensor, Tensor, Tensor)"
 )
 
 
@@ -122,6 +129,13 @@ def _reshape_and_cache_cuda(key: torch.Tensor, value: torch.Tensor, kv_cache: to
     _cache.reshape_and_cache_run(key, value, kv_cache, slot_mapping)
 
 
+def _sample_greedy_fxp_cuda(logits: torch.Tensor, num_logprobs: int, fxp_int_bits: int,
+                            fxp_frac_bits: int):
+    _check_int_bits(fxp_int_bits)
+    _check_frac_bits(fxp_frac_bits)
+    return _sampling.sample_greedy_fxp_run(logits, int(num_logprobs), int(fxp_int_bits), int(fxp_frac_bits))
+
+
 # Register after definition so the functions stay importable by name.
 _lib.impl("float_to_fixed", _float_to_fixed_cuda, "CUDA")
 _lib.impl("fixed_to_float", _fixed_to_float_cuda, "CUDA")
@@ -132,3 +146,4 @@ _lib.impl("unified_attention_fxp", _unified_attention_fxp_cuda, "CUDA")
 _lib.impl("fixed_row_sum", _fixed_row_sum_cuda, "CUDA")
 _lib.impl("log_softmax_fxp", _log_softmax_fxp_cuda, "CUDA")
 _lib.impl("reshape_and_cache", _reshape_and_cache_cuda, "CUDA")
+_lib.impl("sample_greedy_fxp", _sample_greedy_fxp_cuda, "CUDA")

@@ -1,7 +1,7 @@
 """Fake (meta) impls for torch.compile / Dynamo, plus torch.ops.fxpr aliases.
 
 Output shapes and dtypes follow the reference fakes
-(fxpr_vllm/library_ops.py:28-71); the two build-only ops get their own.
+(fxpr_vllm/library_ops.py:28-71); the build-only ops get their own.
 """
 
 from __future__ import annotations
@@ -75,6 +75,14 @@ def _log_softmax_fxp_fake(x, fxp_int_bits, fxp_frac_bits, out_dtype=None):
     return torch.empty_like(x, dtype=x.dtype if out_dtype is None else out_dtype)
 
 
+@torch.library.register_fake("fxpr::sample_greedy_fxp")
+def _sample_greedy_fxp_fake(logits, num_logprobs, fxp_int_bits, fxp_frac_bits):
+    lead = tuple(logits.shape[:-1])
+    k = int(num_logprobs)
+    return (logits.new_empty(lead, dtype=torch.int64), logits.new_empty(lead, dtype=torch.float32),
+            logits.new_empty(lead + (k,), dtype=torch.int64), logits.new_empty(lead + (k,), dtype=torch.float32))
+
+
 @torch.library.register_fake("fxpr::reshape_and_cache")
 def _reshape_and_cache_fake(key, value, kv_cache, slot_mapping):
     return None
@@ -88,4 +96,5 @@ fixed_to_float = torch.ops.fxpr.fixed_to_float
 fixed_row_sum = torch.ops.fxpr.fixed_row_sum
 log_softmax_fxp = torch.ops.fxpr.log_softmax_fxp
 reshape_and_cache = torch.ops.fxpr.reshape_and_cache
+sample_greedy_fxp = torch.ops.fxpr.sample_greedy_fxp
 unified_attention_fxp = torch.ops.fxpr.unified_attention_fxp
