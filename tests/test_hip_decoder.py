@@ -1,76 +1,118 @@
 """End-to-end batch invariance: a random-init Llama-shaped decoder built from
 the fxpr ops (tests/e2e_decoder.py) generates greedily under different
-schedules - every request alone (batch 1), all at once (batch 8 and 32), and a
+schedules - requests alone (batch 1), together (batch 8 and 32), and a
 continuous-batching mix where prefills join running decodes. Every request's
-fixed-point log-probs must be bit-identical across schedules at every step
-(the property the reference's end-to-end config 5 asks for at batch
-1/8/32, with vLLM; here without vLLM)."""
+tokens, sampled-token log-probabilities and top-k log-probabilities (and, for
+the small model, whole fixed-point log-probability rows) must be
+bit-identical across schedules at every step. This is BASELINE config 5's
+property (Llama-3-8B shape, prompts of 2048 tokens, batch 1/8/32) on the
+library's own harness, without vLLM.
+"""
 
 from __future__ import annotations
 
 import pytest
 import torch
 
-from e2e_decoder import Config, TinyDecoder, run
+from e2e_decoder import Config, Decoder, run
 
 pytestmark = pytest.mark.gpu
 
 
-def _prompts(n, seed=0, vocab=1024):
+def _prompts(n, seed=0, vocab=1024, lo=3, hi=40):
     g = torch.Generator("cpu").manual_seed(seed)
-    lens = torch.randint(3, 40, (n,), generator=g).tolist()
+    lens = torch.randint(lo, hi, (n,), generator=g).tolist()
     return [torch.randint(0, vocab, (L,), generator=g).tolist() for L in lens]
 
 
-def _assert_same(a, b):
-    assert a.keys() == b.keys()
-    for rid in a:
-        ra, rb = a[rid], b[rid]
-        assert ra.tokens == rb.tokens, f"request {rid}: tokens differ"
-        assert len(ra.logprobs) == len(rb.logprobs)
-        for s, (x, y) in enumerate(zip(ra.logprobs, rb.logprobs)):
-            assert torch.equal(x.view(torch.int32), y.view(torch.int32)), f"request {rid} step {s}"
+def _bits(t):
+    return t.view(torch.int32) if t.dtype == torch.float32 else t
+
+
+def _assert_same(a, b, what=""):
+    assert a.tokens == b.tokens, f"{what}: tokens differ"
+    assert len(a.logprobs) == len(b.logprobs)
+    for s in range(len(a.logprobs)):
+        assert torch.equal(_bits(a.logprobs[s]), _bits(b.logprobs[s])), f"{what} step {s}: log-prob"
+        assert torch.equal(a.topk[s][0], b.topk[s][0]), f"{what} step {s}: top-k ids"
+        assert torch.equal(_bits(a.topk[s][1]), _bits(b.topk[s][1])), f"{what} step {s}: top-k log-probs"
+    for s, (x, y) in enumerate(zip(a.full, b.full)):
+        assert torch.equal(_bits(x), _bits(y)), f"{what} step {s}: log-prob row"
+
+
+def _alone(step, active):
+    return [min(active, key=lambda r: r.rid)]
+
+
+def _all(step, active):
+    return active
+
+
+def _staggered(step, active):
+    # admit two new requests per step while earlier ones keep decoding
+    return [r for r in active if r.rid < 2 * (step + 1)]
 
 
 def test_batch_1_vs_8_vs_mixed():
     import fxpr_vllm  # noqa: F401
 
+    model = Decoder(Config())
     prompts = _prompts(8)
-    max_new = 6
-
-    def alone_factory():
-        state = {"cur": None}
-
-        def sched(step, active):
-            if state["cur"] is None or state["cur"].done:
-                state["cur"] = min(active, key=lambda r: r.rid)
-            return [state["cur"]]
-        return sched
-
-    def all_at_once(step, active):
-        return active
-
-    def mixed(step, active):
-        # admit two new requests per step while earlier ones keep decoding
-        return [r for r in active if r.rid < 2 * (step + 1)]
-
-    ref = run(TinyDecoder(Config()), prompts, max_new, alone_factory())
-    _assert_same(ref, run(TinyDecoder(Config()), prompts, max_new, all_at_once))
-    _assert_same(ref, run(TinyDecoder(Config()), prompts, max_new, mixed))
+    ref = run(model, prompts, 6, _alone)
+    for name, sched in (("batch 8", _all), ("mixed", _staggered)):
+        got = run(model, prompts, 6, sched)
+        for rid in ref:
+            _assert_same(ref[rid], got[rid], f"{name} request {rid}")
     # the model is not degenerate: requests do not all emit the same tokens
     assert len({tuple(r.tokens[len(r.prompt):]) for r in ref.values()}) > 1
+    # the sampled token is the row's argmax and its log-prob is the row's value
+    for r in ref.values():
+        for s, row in enumerate(r.full):
+            tok = r.tokens[len(r.prompt) + s]
+            assert tok == int(torch.argmax(row)) and torch.equal(_bits(row[tok]), _bits(r.logprobs[s]))
 
 
 def test_batch_32_matches_batch_1_subset():
     import fxpr_vllm  # noqa: F401
 
+    model = Decoder(Config())
     prompts = _prompts(32, seed=1)
-    max_new = 3
-    big = run(TinyDecoder(Config()), prompts, max_new, lambda step, active: active)
-    # the same requests alone, a few of them (each alone is a full generation)
+    big = run(model, prompts, 3, _all)
     for rid in (0, 13, 31):
-        alone = run(TinyDecoder(Config()), [prompts[rid]], max_new, lambda step, active: active)
-        a, b = big[rid], alone[0]
-        assert a.tokens == b.tokens
-        for x, y in zip(a.logprobs, b.logprobs):
-            assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+        _assert_same(big[rid], run(model, [prompts[rid]], 3, _all)[0], f"request {rid}")
+
+
+# --- the Llama-3-8B shape --------------------------------
+
+PROMPT_LEN, BATCH, MAX_NEW = 2048, 32, 16
+
+
+@pytest.fixture(scope="module")
+def llama3_8b():
+    import fxpr_vllm  # noqa: F401
+
+    pages = BATCH * -(-(PROMPT_LEN + MAX_NEW) // 16) + 8
+    model = Decoder(Config.llama3_8b(pages), seed=0)
+    prompts = _prompts(BATCH, seed=5, vocab=128_256, lo=PROMPT_LEN, hi=PROMPT_LEN + 1)
+    yield model, prompts
+    del model
+    torch.cuda.empty_cache()
+
+
+def test_llama3_8b_shape_batch_1_8_32(llama3_8b):
+    # 32 random-token prompts of 2048, greedy 16 tokens with the top-5
+    # log-probabilities: batch 32, its first 8 as batch 8, three requests
+    # alone, and four requests staggered so prefills join running decodes
+    model, prompts = llama3_8b
+    b32 = run(model, prompts, MAX_NEW, _all)
+    b8 = run(model, prompts[:8], MAX_NEW, _all)
+    for rid in range(8):
+        _assert_same(b32[rid], b8[rid], f"batch 8 request {rid}")
+    for rid in (0, 19, 31):
+        _assert_same(b32[rid], run(model, [prompts[rid]], MAX_NEW, _all)[0], f"alone request {rid}")
+    mixed = run(model, prompts[8:12], MAX_NEW, _staggered)
+    for i in range(4):
+        _assert_same(b32[8 + i], mixed[i], f"staggered request {8 + i}")
+    generated = {tuple(r.tokens[PROMPT_LEN:]) for r in b32.values()}
+    assert len(generated) > 1
+    assert all(len(r.tokens) == PROMPT_LEN + MAX_NEW for r in b32.values())
