@@ -205,6 +205,36 @@ int fxpr_unified_attention(
     int window_size, int int_bits, int frac_bits, int num_kv_splits,
     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Size of the device array fxpr_unified_attention_noalloc keeps its split
+ * partials in (per GPU, for the life of the process). */
+#define FXPR_STATIC_SCRATCH_BYTES (64LL << 20)
+
+/*
+ * fxpr_unified_attention without the workspace arguments: allocates nothing.
+ * The split partials go to a static device array of FXPR_STATIC_SCRATCH_BYTES
+ * per GPU; a launch whose fxpr_attention_workspace_bytes() exceeds that is
+ * rejected with FXPR_E_WORKSPACE before anything runs. Same results as
+ * fxpr_unified_attention bit for bit. Calls that overlap on one GPU (two
+ * streams, or two host threads) share the array and race: serialise them.
+ * The stream must belong to the current device or be NULL.
+ * No counterpart in the reference: this is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).
+ */
+int fxpr_unified_attention_noalloc(
+    const void* q, const void* k_cache, const void* v_cache, void* o,
+    int io_dtype, const int32_t* query_start_loc, const int32_t* seq_lens,
+    const int32_t* block_table, const float* alibi_slopes, int num_requests,
+    int64_t num_tokens, int num_heads, int num_kv_heads, int head_dim,
+    int page_size, int max_query_len, int max_blocks_per_seq,
+    int64_t num_blocks, int64_t stride_q_token, int64_t stride_q_head,
+    int64_t stride_k_block, int64_t stride_k_slot, int64_t stride_k_head,
+    int64_t stride_v_block, int64_t stride_v_slot, int64_t stride_v_head,
+    int64_t stride_o_token, int64_t stride_o_head, int64_t stride_bt_row,
+    int is_causal, float softmax_scale_log2, float softcap_log2,
+    int window_size, int int_bits, int frac_bits, int num_kv_splits,
+    void* stream);
+
 /* KV split count for num_kv_splits = requested (0 = automatic).
  * Replaces _pick_num_splits (fxpr_vllm/_triton/attention.py:664-689). */
 int fxpr_attention_splits(int num_requests, int num_kv_heads, int group,

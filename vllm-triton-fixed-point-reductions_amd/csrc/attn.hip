@@ -1,5 +1,7 @@
 // C-ABI entry points of the paged attention (kernels: attn_impl.h,
 // instantiated per input type in attn_{bf16,f16,f32}.hip).
+#include <mutex>
+
 #include "attn_impl.h"
 
 using namespace fxpr;
@@ -201,4 +203,81 @@ extern "C" int fxpr_unified_attention(
     case FXPR_DTYPE_F16: return run_attn_f16(a, int_bits, num_requests, max_qtiles, num_tokens, st);
     default: return run_attn_f32(a, int_bits, num_requests, max_qtiles, num_tokens, st);
   }
+}
+
+// ---------------------------------------------------------------------------
+// The same launch without a caller workspace: split partials go to `scratch`,
+// a file-scope device array of kStaticScratchBytes that each GPU the library
+// runs on holds until the process ends. Its device address is looked up once
+// per device (hipGetSymbolAddress with that device current) and kept in
+// scratch_ptr; host code never passes the array's own name to a kernel. The
+// partials need no zeroing (every slot a combine reads was written by the
+// same launch). Calls that overlap on one GPU share the array and race.
+
+namespace {
+
+constexpr int64_t kStaticScratchBytes = FXPR_STATIC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the stream's device (the current device
+// for the null stream).
+int static_scratch(hipStream_t st, void** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return static_cast<int>(e);
+  int dev = cur;
+  if (st != nullptr) {
+    e = hipStreamGetDevice(st, &dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return FXPR_E_ARG;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return static_cast<int>(e);
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess) return static_cast<int>(e);
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return FXPR_OK;
+}
+
+}  // namespace
+
+extern "C" int fxpr_unified_attention_noalloc(
+    const void* q, const void* k_cache, const void* v_cache, void* o, int io_dtype,
+    const int32_t* query_start_loc, const int32_t* seq_lens, const int32_t* block_table,
+    const float* alibi_slopes, int num_requests, int64_t num_tokens, int num_heads,
+    int num_kv_heads, int head_dim, int page_size, int max_query_len, int max_blocks_per_seq,
+    int64_t num_blocks, int64_t stride_q_token, int64_t stride_q_head, int64_t stride_k_block,
+    int64_t stride_k_slot, int64_t stride_k_head, int64_t stride_v_block, int64_t stride_v_slot,
+    int64_t stride_v_head, int64_t stride_o_token, int64_t stride_o_head, int64_t stride_bt_row,
+    int is_causal, float softmax_scale_log2, float softcap_log2, int window_size, int int_bits,
+    int frac_bits, int num_kv_splits, void* stream) {
+  const int64_t need = fxpr_attention_workspace_bytes(num_requests, num_tokens, num_heads, num_kv_heads,
+                                                      head_dim, int_bits, num_kv_splits, max_query_len,
+                                                      max_blocks_per_seq, page_size);
+  if (need > kStaticScratchBytes) return FXPR_E_WORKSPACE;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = static_scratch(as_stream(stream), &ws);
+    if (rc != FXPR_OK) return rc;
+  }
+  return fxpr_unified_attention(q, k_cache, v_cache, o, io_dtype, query_start_loc, seq_lens, block_table,
+                                alibi_slopes, num_requests, num_tokens, num_heads, num_kv_heads, head_dim,
+                                page_size, max_query_len, max_blocks_per_seq, num_blocks, stride_q_token,
+                                stride_q_head, stride_k_block, stride_k_slot, stride_k_head, stride_v_block,
+                                stride_v_slot, stride_v_head, stride_o_token, stride_o_head, stride_bt_row,
+                                is_causal, softmax_scale_log2, softcap_log2, window_size, int_bits, frac_bits,
+                                num_kv_splits, ws, need, stream);
 }

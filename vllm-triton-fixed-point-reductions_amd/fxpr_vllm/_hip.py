@@ -42,6 +42,9 @@ SIGNATURES: dict[str, list] = {
     "fxpr_unified_attention": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _I, _I, _L,
                                _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L,
                                _I, _F, _F, _I, _I, _I, _I, _P, _L, _P],
+    "fxpr_unified_attention_noalloc": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _I, _I, _L,
+                                       _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L,
+                                       _I, _F, _F, _I, _I, _I, _I, _P],
     "fxpr_attention_splits": [_I, _I, _I, _I, _I, _I, _I],
     "fxpr_reshape_and_cache": [_P, _P, _P, _P, _I, _P, _L, _I, _I, _I, _L,
                                _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P],

@@ -46,7 +46,11 @@ def unified_attention_fxp_run(
     logit_softcap: float,
     window_size: int,
     num_kv_splits: int,
+    static_scratch: bool = False,
 ) -> None:
+    """static_scratch=True calls fxpr_unified_attention_noalloc: no workspace
+    is allocated (the split partials live in the library's static device
+    array; a launch needing more raises RuntimeError)."""
     if not (q.is_cuda and kv_cache.is_cuda and o.is_cuda):
         raise RuntimeError("unified_attention_fxp: tensors must be CUDA")
     if q.dtype not in _SUPPORTED_DTYPES:
@@ -95,13 +99,7 @@ def unified_attention_fxp_run(
     ss_log2 = float(ss) * _RCP_LN2
     softcap_log2 = float(logit_softcap) * _RCP_LN2 if float(logit_softcap) > 0.0 else 0.0
     max_blocks = bt.shape[1]
-    lib = _hip.load()
-    ws_bytes = lib.fxpr_attention_workspace_bytes(num_requests, num_tokens, num_heads, num_kv_heads,
-                                                  head_dim, int(fxp_int_bits), int(num_kv_splits),
-                                                  int(max_query_len), max_blocks, page_size)
-    ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes > 0 else None
-    _hip.call(
-        "fxpr_unified_attention",
+    common = (
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), _hip.DTYPE_CODE[q.dtype],
         qsl.data_ptr(), sl.data_ptr(), bt.data_ptr(), _hip.ptr(alibi),
         num_requests, num_tokens, num_heads, num_kv_heads, head_dim, page_size,
@@ -109,8 +107,15 @@ def unified_attention_fxp_run(
         q.stride(0), q.stride(1), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         v_cache.stride(0), v_cache.stride(1), v_cache.stride(2), out.stride(0), out.stride(1),
         bt.stride(0), int(bool(is_causal)), ss_log2, softcap_log2, max(0, int(window_size)),
-        int(fxp_int_bits), int(fxp_frac_bits), int(num_kv_splits), _hip.ptr(ws), ws_bytes,
-        _hip.stream_ptr(q.device),
+        int(fxp_int_bits), int(fxp_frac_bits), int(num_kv_splits),
     )
+    if static_scratch:
+        _hip.call("fxpr_unified_attention_noalloc", *common, _hip.stream_ptr(q.device))
+    else:
+        ws_bytes = _hip.load().fxpr_attention_workspace_bytes(
+            num_requests, num_tokens, num_heads, num_kv_heads, head_dim, int(fxp_int_bits),
+            int(num_kv_splits), int(max_query_len), max_blocks, page_size)
+        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes > 0 else None
+        _hip.call("fxpr_unified_attention", *common, _hip.ptr(ws), ws_bytes, _hip.stream_ptr(q.device))
     if out is not o:
         o.copy_(out)
