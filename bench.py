@@ -6,18 +6,23 @@
 Prints ONE JSON line. The headline (`metric`/`value`) is BASELINE.json's
 metric: the fixed-point lm_head GEMM in TFLOP/s (bf16 A[8192,4096] x
 B[4096,128256], Q16.16 in int32) whose `roofline` is against the dense bf16
-MFMA peak; the paged split-K decode attention (HBM GB/s and % of roofline),
-RMSNorm+residual and log-softmax lines ride along under `extra`, each with
-its own roofline. A step is one call of the workload's op on one batch of
+MFMA peak; every other BASELINE configuration rides along under `extra`
+with its own roofline: the paged split-K decode attention at each split count
+(HBM GB/s), the other GEMM shapes, RMSNorm + residual and log-softmax (HBM),
+causal prefill attention (MFMA), config 1's cast / row-sum / RMSNorm chain,
+and config 5's Llama-3-8B-shaped decoder (tokens/s, report only). A step is one call of the workload's op on one batch of
 seeded synthetic input already resident in HBM; each workload times exactly K
 steps between HIP events recorded on the stream the kernels run on, after W
 warmup steps, with a device synchronize on both sides. Inputs whose total
 footprint would fit in the 256 MB MALL are rotated across copies so the
 figures are HBM figures.
 
-`cpu_baseline` times the numpy oracle (oracle/, the CPU restatement of the
-same fixed-point arithmetic) on a bounded sample of the headline workload on
-this box's host cores.
+`cpu_baseline` is the CPU emulation of the headline's fixed-point path
+(oracle/torch_cpu.py, PyTorch on every host thread, pinned bit for bit to the
+numpy oracle) timed on this box's host cores on a column slice of the
+headline shape, extrapolated and labelled; `cpu_suite` holds the same
+emulation timed per BASELINE configuration (configs 1, 2a, 4 and GEMM
+M <= 32 whole, the rest on labelled samples), with the thread count of each.
 """
 
 from __future__ import annotations
@@ -102,19 +107,25 @@ def hbm_roofline(bytes_per_call: float, ms: float) -> dict:
 
 
 def measured_traffic(workload: str):
-    """HBM bytes per launch of the workload's dominant kernel, from the
-    rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs summarised in
-    profiles/hbm_traffic.md (counter KiB scaled by the factor a plain copy of
-    known size reads), or None when the workload was not profiled."""
+    """(HBM bytes per launch of the workload's dominant kernel, where that
+    figure comes from): the rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs
+    summarised in profiles/hbm_traffic.md (counter KiB scaled by the factor a
+    plain copy of known size reads), stamped with the commit of the kernels
+    it measured; (None, None) when the workload was not profiled. A counter
+    run cannot share the process it measures, so the figure is not re-taken
+    here."""
     path = ROOT / "profiles" / "hbm_traffic.md"
     try:
-        for line in path.read_text().splitlines():
+        text = path.read_text()
+        stamp = next((ln.split(":", 1)[1].strip() for ln in text.splitlines()
+                      if ln.lower().startswith("kernels measured at commit")), "unknown commit")
+        for line in text.splitlines():
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
             if len(cells) >= 5 and cells[0] == f"`{workload}`":
-                return int(cells[-1].replace(",", ""))
+                return int(cells[-1].replace(",", "")), f"profiles/hbm_traffic.md ({stamp})"
     except (OSError, ValueError):
         pass
-    return None
+    return None, None
 
 
 def mfma_roofline(flops: float, ms: float, peak: float = BF16_PEAK_TFLOPS) -> dict:
@@ -300,6 +311,108 @@ def wl_prefill(steps, warmup, splits=0, int_bits=32, frac_bits=16, B=4, L=2048, 
             "ms": round(ms, 5), "flops": flops, "roofline": mfma_roofline(flops, ms, BF16_PEAK_TFLOPS)}
 
 
+def wl_config1(steps, warmup, int_bits=32):
+    """BASELINE config 1 on the GPU: fp32 x [4096, 4096] ~N(0,1) through
+    float_to_fixed -> fixed_row_sum -> fixed_to_float (Q16.16 in int32 or
+    int64), then RMSNorm and RMSNorm + residual (weight ~N(1, 0.1), eps 1e-6),
+    one step = the five launches. Algorithmic bytes: the cast reads 4 n and
+    writes b/8 n, the row sum reads b/8 n, RMSNorm moves 8 n, RMSNorm +
+    residual 16 n (n = 4096^2; the [4096] results are negligible)."""
+    import torch
+
+    n = 4096
+    g = torch.Generator("cpu").manual_seed(0)
+    x = torch.randn(n, n, generator=g).to("cuda")
+    r0 = torch.randn(n, n, generator=g).to("cuda")
+    w = (torch.randn(n, generator=g) * 0.1 + 1.0).to("cuda")
+    nb = int_bits // 8
+    nbytes = n * n * (4 + nb + nb + 8 + 16)
+    sets = [(x, r0.clone(), w) for _ in range(copies_for(nbytes))]
+
+    def fn(xx, rr, ww):
+        q = torch.ops.fxpr.float_to_fixed(xx, int_bits, 16)
+        torch.ops.fxpr.fixed_to_float(torch.ops.fxpr.fixed_row_sum(q, int_bits), 32, 16)
+        torch.ops.fxpr.rms_norm_fxp(xx, ww, 1e-6)
+        torch.ops.fxpr.rms_norm_fxp_residual(xx, rr, ww, 1e-6)
+
+    ms = time_op(fn, sets, steps, warmup)
+    return {"workload": f"config 1: fp32 [{n},{n}] cast -> row sum -> cast (Q16.16 in int{int_bits}), "
+                        f"RMSNorm, RMSNorm + residual",
+            "ms": round(ms, 5), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms)}
+
+
+def wl_e2e_llama(steps, warmup, batch=32, prompt=2048):
+    """BASELINE config 5 on the library's own harness (tests/e2e_decoder.py):
+    a random-init Llama-3-8B-shaped decoder (32 layers, hidden 4096, 32/8
+    heads of 128, FFN 14336, vocab 128256, bf16 weights ~N(0, 0.02)) built
+    only from the fxpr ops, `batch` random-token prompts of `prompt` tokens
+    prefilled in one step, then greedy decode steps of the whole batch (the
+    sampler with top-5 log-probabilities). Reported: decode tokens/s (a step =
+    one decode token for every request) and the prefill's tokens/s."""
+    import torch
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from e2e_decoder import Config, Decoder, Request
+
+    pages = batch * -(-(prompt + steps + warmup + 1) // 16) + 8
+    model = Decoder(Config.llama3_8b(pages), seed=0)
+    g = torch.Generator("cpu").manual_seed(5)
+    prompts = [torch.randint(0, 128256, (prompt,), generator=g).tolist() for _ in range(batch)]
+    reqs = [Request(i, p, 1 << 30, tokens=list(p)) for i, p in enumerate(prompts)]
+    dev = "cuda"
+    free = list(range(pages))
+    max_pages = -(-(prompt + steps + warmup + 1) // 16)
+
+    def forward():
+        toks, pos, slots, qsl, sls, bts = [], [], [], [0], [], []
+        for rq in reqs:
+            new = rq.tokens[rq.cached:]
+            while len(rq.pages) < -(-len(rq.tokens) // 16):
+                rq.pages.append(free.pop(0))
+            for j, t in enumerate(new):
+                p = rq.cached + j
+                toks.append(t)
+                pos.append(p)
+                slots.append(rq.pages[p // 16] * 16 + p % 16)
+            qsl.append(qsl[-1] + len(new))
+            sls.append(len(rq.tokens))
+            bts.append(rq.pages + [0] * (max_pages - len(rq.pages)))
+        last = [qsl[i + 1] - 1 for i in range(len(reqs))]
+        ids = model.step(torch.tensor(toks, device=dev), torch.tensor(pos, device=dev),
+                         torch.tensor(qsl, dtype=torch.int32, device=dev),
+                         torch.tensor(sls, dtype=torch.int32, device=dev),
+                         torch.tensor(bts, dtype=torch.int32, device=dev),
+                         torch.tensor(slots, dtype=torch.int64, device=dev),
+                         max(qsl[i + 1] - qsl[i] for i in range(len(reqs))), torch.tensor(last, device=dev))[0].cpu()
+        for i, rq in enumerate(reqs):
+            rq.cached = len(rq.tokens)
+            rq.tokens.append(int(ids[i]))
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    forward()                      # prefill of every prompt
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    for _ in range(warmup):
+        forward()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        forward()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": f"config 5: Llama-3-8B-shaped decoder on the fxpr ops, batch {batch}, prompts {prompt}, "
+                        f"greedy decode (top-5 log-probs)",
+            "ms": round(ms, 5), "decode_tokens_per_s": round(batch / (ms * 1e-3), 1),
+            "prefill_tokens_per_s": round(batch * prompt / prefill_s, 1),
+            "roofline": {"bound": "mixed", "achieved": round(batch / (ms * 1e-3), 1), "peak": None,
+                         "unit": "tokens/s", "frac": None, "traffic": None}}
+
+
 def wl_hbm_copy(steps, warmup, nbytes=1 << 30):
     """torch copy_ of a known size: the reference point for HBM bandwidth and
     for scaling the FETCH_SIZE / WRITE_SIZE counters."""
@@ -331,64 +444,146 @@ WORKLOADS = {
     "rms_norm": lambda s, w: wl_rms_norm(s, w),
     "log_softmax": lambda s, w: wl_log_softmax(s, w, 32, 16),
     "log_softmax_f32out_q32i64": lambda s, w: wl_log_softmax(s, w, 64, 32, fp32_out=True),
+    "config1_q16_i32": lambda s, w: wl_config1(s, w, 32),
+    "config1_q16_i64": lambda s, w: wl_config1(s, w, 64),
+    "e2e_llama3_8b": lambda s, w: wl_e2e_llama(min(s, 8), 2),
     "hbm_copy": lambda s, w: wl_hbm_copy(s, w),
 }
 HEADLINE_ORDER = ["gemm_lm_head", "decode_attn", "rms_norm"]
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the numpy oracle on a bounded sample of the headline workload
+# CPU baseline: the CPU emulation of the same fixed-point path, timed per
+# BASELINE configuration on this box's host cores. GEMM, RMSNorm,
+# log-softmax and the casts run as PyTorch CPU code on every host thread
+# (oracle/torch_cpu.py, pinned bit for bit to the numpy oracle); the decode
+# attention runs as the numpy oracle (oracle/attention.py, one core). Shapes
+# too slow to run whole are timed on a documented sample and extrapolated
+# linearly in the sampled dimension; each entry says which.
 
 
-def cpu_baseline(headline: str, budget_s: float) -> dict:
+def _timed(fn, min_s: float = 0.0):
+    """(seconds per call, calls): at least one call, repeated up to min_s."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        if time.perf_counter() - t0 >= min_s:
+            return (time.perf_counter() - t0) / n, n
+
+
+def cpu_suite(scale: float = 1.0) -> dict:
+    """Per-configuration CPU timings. `scale` multiplies the sample sizes of
+    the extrapolated entries (1.0: about a minute in all)."""
     import numpy as np
+    import torch
 
-    from oracle import rows as OR
+    from oracle import attention as OA
+    from oracle import numerics as ON
+    from oracle import torch_cpu as TC
 
-    threads = 1  # numpy elementwise arithmetic runs on one core
-    if headline.startswith("gemm"):
-        from oracle import gemm as OG
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    torch.randn(1 << 20).sum()   # start the thread pool outside the timed calls
+    g = torch.Generator("cpu").manual_seed(0)
+    out = {}
 
-        try:
-            from threadpoolctl import threadpool_info
+    def randn(*shape, std=1.0, mean=0.0):
+        return torch.randn(*shape, generator=g) * std + mean
 
-            threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-        except Exception:  # noqa: BLE001
-            threads = os.cpu_count() or 1
-        M, K, Nn = 64, 4096, 2048
-        rng = np.random.default_rng(0)
-        a = (rng.standard_normal((M, K)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
-        b = ((rng.standard_normal((K, Nn)) * 0.02).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            OG.gemm(a, b, None, "bf16", 32, 16)
-            reps += 1
-            if time.perf_counter() - t0 > budget_s:
-                break
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(2.0 * M * K * Nn / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
-                "kind": "port",
-                "sample": f"oracle.gemm.gemm bf16 A[{M},{K}] x B[{K},{Nn}] Q16/i32 (numpy, BLAS "
-                          f"float64 tile dots), {reps} reps in {budget_s:.0f}s"}
-    if headline.startswith("rms_norm"):
-        H = 4096
-        rows = 64
-        rng = np.random.default_rng(0)
-        x = (rng.standard_normal((rows, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
-        r = (rng.standard_normal((rows, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
-        w = np.full(H, 0x3F80, np.uint16)
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            OR.rms_norm(x, w, 1e-6, "bf16", residual=r)
-            reps += 1
-            if time.perf_counter() - t0 > budget_s:
-                break
-        dt = (time.perf_counter() - t0) / reps
-        gbs = 4 * rows * H * 2 / dt / 1e9
-        return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": f"oracle.rows.rms_norm bf16 [{rows},{H}] + residual, "
-                          f"{reps} reps in {budget_s:.0f}s"}
-    raise ValueError(headline)
+    def bf16(t):
+        return TC.store(t, "bf16")
+
+    def entry(value, unit, seconds, cores, sample, extrapolated=False, impl="torch_cpu"):
+        return {"value": round(value, 6), "unit": unit, "seconds_full_shape": round(seconds, 4), "cores": cores,
+                "kind": "port", "impl": impl, "sample": sample, "extrapolated": extrapolated}
+
+    # config 1: fp32 [4096, 4096] cast -> row sum -> cast; RMSNorm + residual
+    n = 4096
+    x, r, w = randn(n, n), randn(n, n), randn(n, std=0.1, mean=1.0)
+    for bits in (32, 64):
+        dt, _ = _timed(lambda: TC.fixed_to_f32(TC.fixed_row_sum(TC.float_to_fixed(x, bits, 16), bits), 16))
+        nbytes = 4 * n * n + (bits // 8) * n * n * 2
+        out[f"config1_cast_rowsum_q16_i{bits}"] = entry(nbytes / dt / 1e9, "GB/s", dt, threads,
+                                                         f"full [{n},{n}] fp32, Q16.16 in int{bits}")
+    dt, _ = _timed(lambda: TC.rms_norm(x, w, 1e-6, "f32", residual=r))
+    out["config1_rms_norm_residual_f32"] = entry(16 * n * n / dt / 1e9, "GB/s", dt, threads, f"full [{n},{n}] fp32")
+
+    # config 2a: RMSNorm + residual, bf16 [16384, 4096]
+    T, H = 16384, 4096
+    xb, rb, wb = bf16(randn(T, H)), bf16(randn(T, H)), bf16(randn(H, std=0.1, mean=1.0))
+    dt, _ = _timed(lambda: TC.rms_norm(xb, wb, 1e-6, "bf16", residual=rb))
+    out["config2a_rms_norm_residual_bf16"] = entry(4 * T * H * 2 / dt / 1e9, "GB/s", dt, threads,
+                                                   f"full [{T},{H}] bf16")
+    del xb, rb
+
+    # config 2b: log-softmax, bf16 [256, 128256] ~N(0,4) with 1 % at +-30
+    R, V = 256, 128256
+    rs = max(8, int(64 * scale))
+    lg = randn(rs, V, std=4.0)
+    lg = torch.where(torch.rand(rs, V, generator=g) < 0.01, torch.full_like(lg, 30.0), lg)
+    lgb = bf16(lg)
+    for bits, frac in ((32, 16), (64, 32)):
+        dt, _ = _timed(lambda: TC.log_softmax(lgb, "bf16", "bf16", bits, frac))
+        full = dt * R / rs
+        out[f"config2b_log_softmax_q{frac}_i{bits}"] = entry(R * V * 4 / full / 1e9, "GB/s", full, threads,
+                                                              f"{rs} of {R} rows x {V}, bf16 in and out",
+                                                              rs != R)
+
+    # config 3: lm_head GEMM, bf16 A[M, 4096] x B[4096, 128256]; M <= 32 whole,
+    # larger M on a column slice of B (time linear in N)
+    K, N = 4096, 128256
+    wfull = bf16(randn(K, N, std=0.02))
+    for M in (1, 32, 256, 2048, 8192):
+        ncols = N if M <= 32 else max(128, int({256: 16384, 2048: 2048, 8192: 512}[M] * scale))
+        a = bf16(randn(M, K))
+        bsl = wfull if ncols == N else wfull[:, :ncols].contiguous()
+        dt, _ = _timed(lambda: TC.gemm(a, bsl, None, "bf16", 32, 16))
+        full = dt * N / ncols
+        out[f"config3_gemm_bf16_m{M}"] = entry(2.0 * M * K * N / full / 1e12, "TFLOP/s", full, threads,
+                                               f"A[{M},{K}] x B[{K},{ncols}] of N={N}, Q16.16 in int32",
+                                               ncols != N)
+    del wfull
+    # config 3': f16 / fp32 A[8192, 4096] x B[4096, 14336] on a column slice
+    for io in ("f16", "f32"):
+        M, N2 = 8192, 14336
+        nc = max(128, int(512 * scale))
+        a = TC.store(randn(M, K), io)
+        bsl = TC.store(randn(K, nc, std=0.02), io)
+        dt, _ = _timed(lambda: TC.gemm(a, bsl, None, io, 32, 16))
+        full = dt * N2 / nc
+        out[f"config3p_gemm_{io}_m{M}"] = entry(2.0 * M * K * N2 / full / 1e12, "TFLOP/s", full, threads,
+                                                f"A[{M},{K}] x B[{K},{nc}] of N={N2}, Q16.16 in int32", True)
+
+    # config 4: decode attention, 64 one-token requests with the GPU bench's
+    # seeded context lengths U[512, 8192], 16-token pages, whole (numpy oracle)
+    gl = torch.Generator("cpu").manual_seed(0)
+    sl = torch.randint(512, 8193, (64,), generator=gl, dtype=torch.int32).numpy()
+    nbk = [-(-int(L) // 16) for L in sl]
+    rng = np.random.default_rng(0)
+    kv = ON.store(rng.standard_normal((sum(nbk), 2, 16, 8, 128)).astype(np.float32), "bf16")
+    bt = np.zeros((64, max(nbk)), np.int32)
+    off = 0
+    for i, nb in enumerate(nbk):
+        bt[i, :nb] = np.arange(off, off + nb)
+        off += nb
+    q = ON.store(rng.standard_normal((64, 32, 128)).astype(np.float32), "bf16")
+    qsl = np.arange(65, dtype=np.int32)
+    dt, _ = _timed(lambda: OA.unified_attention(q, kv, qsl, sl, bt, "bf16", softmax_scale=128 ** -0.5,
+                                                chunk_keys=OA.CHUNK_KEYS))
+    nbytes = int(sl.sum()) * 4096 + 2 * 64 * 32 * 128 * 2
+    out["config4_decode_attention"] = entry(nbytes / dt / 1e9, "GB/s", dt, 1,
+                                            f"full: 64 requests, sum of contexts {int(sl.sum())}",
+                                            impl="numpy oracle")
+    return out
+
+
+def cpu_baseline_from(suite: dict, headline: str) -> dict:
+    key = {"gemm_lm_head": "config3_gemm_bf16_m8192", "decode_attn": "config4_decode_attention",
+           "rms_norm": "config2a_rms_norm_residual_bf16"}[headline]
+    e = dict(suite[key])
+    e["config"] = key
+    return e
 
 
 def main() -> None:
@@ -397,7 +592,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workloads", default="all")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-scale", type=float, default=1.0,
+                    help="sample size factor of the extrapolated CPU baseline entries")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
 
@@ -422,7 +618,10 @@ def main() -> None:
         log(f"workload {name} ...")
         _SETTLE_S = 0.0 if name == headline else 0.2  # the headline: exactly W warmup steps
         results[name] = WORKLOADS[name](args.steps, args.warmup)
-        results[name]["roofline"]["traffic"] = measured_traffic(name)
+        traffic, source = measured_traffic(name)
+        results[name]["roofline"]["traffic"] = traffic
+        if traffic is not None:
+            results[name]["roofline"]["traffic_source"] = source
         log(f"  {json.dumps(results[name])}")
 
     _WEIGHTS.clear()
@@ -451,8 +650,11 @@ def main() -> None:
                  "gpu": torch.cuda.get_device_name(0)},
     }
     if not args.no_cpu:
-        log("cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(headline, args.cpu_seconds)
+        log("cpu baseline (oracle per configuration) ...")
+        suite = cpu_suite(args.cpu_scale)
+        out["cpu_baseline"] = cpu_baseline_from(suite, headline)
+        out["cpu_suite"] = suite
+        log(f"  {json.dumps(suite)}")
     print(json.dumps(out), flush=True)
 
 
