@@ -109,14 +109,28 @@ constexpr int kLsmThreads = 512;
 // [2^23, 2^24), spacing 1; the constant is even), no saturation occurs, and
 // NaN d was raised to the floor as in exp_scaled_to_round. Returns the sum's
 // bit pattern, i.e. the quantised value + 0x4B400000.
+// k = rint(t) is taken by the same constant: fl(t + 1.5 * 2^23) - 1.5 * 2^23
+// is t rounded half to even (|t| < 116), and the sum's bit pattern is
+// 0x4B400000 + k, from which one add-and-shift forms 2^(k+f).
+// The caller guarantees d >= exp_zero_below(f) (> -80) or discards the
+// result, so the floor clamp of exp_scaled_to_round is not needed here.
 __device__ __forceinline__ uint32_t exp_scaled_rc_bits(float d, int f) {
-  d = fmaxf(d, FXPR_EXP_FLOOR);  // maxNum: NaN -> the floor
   const float t = __fmul_rn(d, FXPR_LOG2E);
-  const float k = __builtin_rintf(t);
+  const float tk = __fadd_rn(t, 12582912.0f);
+  const float k = __fsub_rn(tk, 12582912.0f);
   const float r = __fsub_rn(t, k);
-  const float s2 = __uint_as_float(static_cast<uint32_t>(static_cast<int>(k) + f + 127) << 23);
-  return __float_as_uint(__builtin_fmaf(exp2_poly(r), s2, 12582912.0f));
+  uint32_t s2bits;
+  asm("v_add_lshl_u32 %0, %1, %2, 23" : "=v"(s2bits) : "v"(tk), "s"(uint32_t(f + 127) - 0x4B400000u));
+  return __float_as_uint(__builtin_fmaf(exp2_poly(r), __uint_as_float(s2bits), 12582912.0f));
 }
+
+// A term whose difference to the row maximum is below this quantises to
+// exactly 0, so it may be skipped: for d < -(f + 1) ln 2 - 1/16 the exact
+// e^d * 2^f is below 0.5 * e^(-1/16) = 0.4697, and the computed value is
+// within 6e-6 of it relatively (t = fl(d * log2 e) is off by at most
+// 115 * 2^-24 absolutely, the polynomial and its roundings by about 1e-7), so
+// it rounds to 0 (and a NaN difference, which compares false, also gives 0).
+__host__ __device__ inline float exp_zero_below(int f) { return -(f + 1) * 0.69314718056f - 0.0625f; }
 
 // fl32(v), round half to even, for an unsigned 64- or 128-bit integer. A
 // 128-bit value beyond 64 bits is shifted into 64 bits with the dropped bits
@@ -173,6 +187,12 @@ __device__ __forceinline__ float row_lse(const Vec<typename Io<XDT>::T, VEC>* __
   }
   m = block_max(m, fred);
 
+  // On the rounding-constant path the wave computes an element slot's exp
+  // only when some lane's difference reaches exp_zero_below (a uniform
+  // branch: peaked rows skip most slots); the terms it skips are exactly 0.
+  // The exact path stays branch-free (its thresholds, for large f, skip
+  // little).
+  const float zero_below = exp_zero_below(frac);
   SumT acc = 0;
   auto accum = [&](const XV& xv) {
 #pragma unroll
@@ -185,8 +205,13 @@ __device__ __forceinline__ float row_lse(const Vec<typename Io<XDT>::T, VEC>* __
     uint32_t acc32 = 0;
     auto accum_rc = [&](const XV& xv) {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j)
-        acc32 += exp_scaled_rc_bits(__fsub_rn(Io<XDT>::load(xv.v[j]), m), frac) - 0x4B400000u;
+      for (int j = 0; j < VEC; ++j) {
+        const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
+        if (__builtin_amdgcn_ballot_w64(d >= zero_below) != 0) {
+          const uint32_t q = exp_scaled_rc_bits(d, frac) - 0x4B400000u;
+          acc32 += d >= zero_below ? q : 0u;
+        }
+      }
     };
 #pragma unroll
     for (int i = 0; i < NREG; ++i) {
