@@ -57,6 +57,28 @@ def test_writes_count_in_order_and_unrelated_registers_pass():
     assert hits == []
 
 
+def test_lds_address_that_is_a_pending_destination_is_reported():
+    # two reads in one asm statement whose outputs are not early-clobber:
+    # the compiler may make the first read's destination the second's
+    # address, which the first read overwrites if it lands first
+    hits = _scan("""
+        ds_read_u16 v1, v0
+        ds_read_b32 v0, v1
+        s_waitcnt lgkmcnt(0)
+    """)
+    assert len(hits) == 1 and "ds_read_b32 v0, v1" in hits[0]
+    # a write's data register counts as well; distinct registers pass
+    assert len(_scan("""
+        ds_read_b32 v1, v0
+        ds_write_b32 v2, v1
+    """)) == 1
+    assert _scan("""
+        ds_read_u16 v1, v0
+        ds_read_b32 v2, v3
+        s_waitcnt lgkmcnt(0)
+    """) == []
+
+
 def test_no_fall_through_after_an_unconditional_branch():
     hits = _scan("""
         ds_read_b128 v[0:3], v10

@@ -10,7 +10,8 @@ an inline-asm read's destination is ready at issue, so nothing but the kernel's
 structure stops it from copying or reading that register before the wait that
 covers it, which would use stale data. This script compiles the sources to
 gfx950 assembly with the build's flags and scans each DMA kernel in program
-order: a vector instruction touching the destination of a ds_read that no
+order: a vector instruction (an LDS one included: its address or data) touching
+the destination of a ds_read that no
 lgkmcnt wait has covered yet (LDS operations complete in issue order, so
 lgkmcnt(N) covers all but the N newest) is reported. The scan follows the text
 and its fall-through edges, not the branches: after an unconditional branch
@@ -75,6 +76,16 @@ def scan_kernel(lines: list[str]) -> list[str]:
             continue
         if op.startswith("ds_"):
             ops = rest.split()
+            # an LDS instruction's own operands (a read's address, a write's
+            # address and data) must not be a pending read's destination
+            # either: it may issue after that read has landed
+            srcs = ops[1:] if op.startswith("ds_read") else ops
+            used = set()
+            for tok in srcs:
+                used |= _vregs(tok)
+            live = set().union(*pending) if pending else set()
+            if used & live:
+                found.append(f"{t}  (in flight: v{sorted(used & live)})")
             pending.append(_vregs(ops[0]) if op.startswith("ds_read") and ops else set())
             continue
         if op in ("s_branch", "s_endpgm", "s_setpc_b64"):

@@ -673,6 +673,50 @@ __device__ __forceinline__ void lds_wait_for(A& a, B& b, C& c, D& d) {
 // is nt (non-temporal; glc/sc0 is bit 0, sc1 bit 4).
 constexpr int kCpolNT = 2;
 
+// Requests in launch order longest first (by sequence length, ties by index)
+// for up to kOrderMax of them: request_by_length(a, k) is the k-th longest,
+// so the workgroups of the requests that bound the launch are dispatched
+// first, and (with two workgroups per CU placed in dispatch order) a long
+// request's workgroup tends to share its CU with a short one's. Wave-uniform;
+// each wave ranks 64 requests per pass with scalar loads of the lengths
+// (about half a microsecond: launches whose workgroups hold at most one
+// chunk each keep the launch order, the ranking would cost more than the
+// order gains).
+constexpr int kOrderMax = 256;
+__device__ __forceinline__ int request_by_length(const AttnArgs& a, int k) {
+  const int R = a.num_requests;
+  const int per_max = a.num_splits <= 1 ? a.chunk_slots + 1
+                      : a.chunks_per_split > 0 ? a.chunks_per_split
+                                               : (a.chunk_slots + a.num_splits - 1) / a.num_splits;
+  if (R <= 1 || R > kOrderMax || per_max <= 1) return k;
+  const ConstI32Ptr sls = (ConstI32Ptr)a.seq_lens;
+  const int lane = threadIdx.x & 63;
+  for (int i0 = 0; i0 < R; i0 += 64) {
+    const int i = i0 + lane;
+    const int li = i < R ? a.seq_lens[i] : 0;
+    int rank = 0;
+    for (int kk = 0; kk < R; ++kk) {
+      const int lk = sls[kk];
+      rank += (lk > li || (lk == li && kk < i)) ? 1 : 0;
+    }
+    const uint64_t m = __builtin_amdgcn_ballot_w64(i < R && rank == k);
+    if (m) return i0 + __builtin_ctzll(m);
+  }
+  return k;  // not reached: ranks are a permutation of 0 .. R - 1
+}
+
+// Wait for the DMAs of a step when `later` steps' DMAs (NDMA instructions
+// each) were issued after it, at most K of them; and for every LDS / scalar
+// memory operation.
+template <int K, int NDMA> __device__ __forceinline__ void dma_wait(int later) {
+  if constexpr (K == 0) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  } else {
+    if (later >= K) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(K * NDMA) : "memory");
+    else dma_wait<K - 1, NDMA>(later);
+  }
+}
+
 template <int DT, int BITS, int DMAX, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   static_assert(DT != FXPR_DTYPE_F32, "16-bit inputs only");
@@ -694,7 +738,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(smem_raw));
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, kg = lane >> 4;
-  const int r = blockIdx.x / a.num_kv_heads, g = blockIdx.x % a.num_kv_heads;
+  const int g = blockIdx.x % a.num_kv_heads;
+  const int r = request_by_length(a, blockIdx.x / a.num_kv_heads);
   const int qt = blockIdx.y, split = blockIdx.z;
   const int q_start = a.qsl[r];
   const int q_len = a.qsl[r + 1] - q_start;
@@ -767,19 +812,24 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
       isv = false;
       t = live_lo(cc);
     } else {
-      t = live_hi(cc) - 1;  // past the end: re-issue the last tile
+      t = live_hi(cc) - 1;  // past the end (no DMA is issued there)
     }
   };
   int dc_ = my_lo, dt = my_lo < my_hi ? live_lo(my_lo) : 0;  // DMA cursor
   bool dv = false;
   int dent = 0;  // page entry at the cursor
+  // steps of this workgroup: per chunk its live K tiles, then the same V tiles
+  int total_steps = 0;
+  for (int c = my_lo; c < my_hi; ++c) total_steps += 2 * (live_hi(c) - live_lo(c));
   if (my_lo < my_hi) {
     dent = page_entry(dt);
 #pragma unroll
     for (int i = 0; i + 1 < NS; ++i) {
-      dma_tile(dv, dt, dent, i);
-      advance(dc_, dv, dt);
-      dent = page_entry(dt);
+      if (i < total_steps) {
+        dma_tile(dv, dt, dent, i);
+        advance(dc_, dv, dt);
+        dent = page_entry(dt);
+      }
     }
   }
 
@@ -853,9 +903,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
 
   if (my_lo < my_hi) {
     // Steps: per chunk its live K tiles, then the same V tiles. Step s uses
-    // stage s % NS; its DMAs were issued NS - 1 steps earlier (past the last
-    // step the last tile is re-issued into the free stage, so every step
-    // issues the same number of DMAs and the wait count stays exact).
+    // stage s % NS; its DMAs were issued NS - 1 steps earlier, and each step
+    // waits for them knowing how many steps' DMAs went out after them (NS - 2,
+    // fewer for the last steps: nothing is issued past the last step).
 
     float sc[CT][4];
     float mx[4];
@@ -874,13 +924,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) wv[b][e] = 0;
       auto step_begin = [&]() -> unsigned {
-        // own DMAs of this step landed (only later steps' in flight), own
+        // own DMAs of this step landed (only later steps' in flight: the
+        // last steps have fewer after them, no DMA goes past the end), own
         // LDS writes done; the barrier makes both everyone's
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(G::NDMA * (NS - 2)) : "memory");
+        dma_wait<NS - 2, G::NDMA>(total_steps - 1 - step);
         __builtin_amdgcn_s_barrier();
-        dma_tile(dv, dt, dent, (step + NS - 1) % NS);
-        advance(dc_, dv, dt);
-        dent = page_entry(dt);  // for the next step's DMAs
+        if (step + NS - 1 < total_steps) {
+          dma_tile(dv, dt, dent, (step + NS - 1) % NS);
+          advance(dc_, dv, dt);
+          dent = page_entry(dt);  // for the next step's DMAs
+        }
         const unsigned base = lds0 + (step % NS) * G::TILEB;
         ++step;
         return base;
@@ -950,24 +1003,44 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
       for (int u = 0; u < CT; ++u) {
         if (u < nt) {
           const unsigned base = step_begin();
+          static_assert(DB_PER_WAVE * 4 == DBLK && NK0 == 2, "every wave owns whole d blocks");
+          // all of the step's LDS reads (the weights once for every d block),
+          // one wait, then the MFMA chains
+          u32x4 pa[NK0];
+          uint64_t vlo[DB_PER_WAVE][NK0], vhi[DB_PER_WAVE][NK0];
+#pragma unroll
+          for (int s = 0; s < NK0; ++s)
+            lds_read_b128(lds0 + PS_OFF + (((u & 1) * QROWS + (lane & 15)) * VP + s * KI + 8 * kg) * 2, pa[s]);
+#pragma unroll
+          for (int b = 0; b < DB_PER_WAVE; ++b)
+#pragma unroll
+            for (int s = 0; s < NK0; ++s) {
+              lds_read_b64_tr16(base + voff[b][s][0], vlo[b][s]);
+              lds_read_b64_tr16(base + voff[b][s][1], vhi[b][s]);
+            }
+          if constexpr (DB_PER_WAVE == 2)
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(pa[0]), "+v"(pa[1]), "+v"(vlo[0][0]), "+v"(vlo[0][1]), "+v"(vlo[1][0]),
+                           "+v"(vlo[1][1]), "+v"(vhi[0][0]), "+v"(vhi[0][1]), "+v"(vhi[1][0]), "+v"(vhi[1][1])
+                         :
+                         : "memory");
+          else
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(pa[0]), "+v"(pa[1]), "+v"(vlo[0][0]), "+v"(vlo[0][1]), "+v"(vhi[0][0]),
+                           "+v"(vhi[0][1])
+                         :
+                         : "memory");
 #pragma unroll
           for (int b = 0; b < DB_PER_WAVE; ++b) {
-            if (wave + 4 * b < DBLK) {
-              f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-              for (int s = 0; s < NK0; ++s) {
-                u32x4 pa;
-                uint64_t lo2, hi2;
-                lds_read_b128(lds0 + PS_OFF + (((u & 1) * QROWS + (lane & 15)) * VP + s * KI + 8 * kg) * 2, pa);
-                lds_read_b64_tr16(base + voff[b][s][0], lo2);
-                lds_read_b64_tr16(base + voff[b][s][1], hi2);
-                lds_wait_for(pa, lo2, hi2);
-                const u32x4 vb = {uint32_t(lo2), uint32_t(lo2 >> 32), uint32_t(hi2), uint32_t(hi2 >> 32)};
-                acc = TR::mma(pa, vb, acc);
-              }
-#pragma unroll
-              for (int e = 0; e < 4; ++e) wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+            for (int s = 0; s < NK0; ++s) {
+              const u32x4 vb = {uint32_t(vlo[b][s]), uint32_t(vlo[b][s] >> 32), uint32_t(vhi[b][s]),
+                                uint32_t(vhi[b][s] >> 32)};
+              acc = TR::mma(pa[s], vb, acc);
             }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wv[b][e] = wadd<BITS>(wv[b][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
           }
           if (u + 1 < nt) write_p(u + 1);
         }
