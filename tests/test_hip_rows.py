@@ -350,6 +350,51 @@ def test_log_softmax_flat_full_vocab_row(b, f):
         assert abs(torch.exp(got.double()).sum(-1) - 1).max().item() < V * 2.0 ** -(f + 1) + 1e-5
 
 
+def test_log_softmax_split_rows_equal_one_workgroup_rows():
+    # up to 1024 rows of at least 4096 16-byte vectors are shared by 2..16
+    # workgroups each (span maxima and exact span sums exchanged through
+    # device memory); 1025 rows take one workgroup per row: same bits
+    x = _logits(1025, 32_768, seed=11).to(DEV)
+    for b, f in ((32, 16), (64, 32)):
+        one = torch.ops.fxpr.log_softmax_fxp(x, b, f)
+        split = torch.ops.fxpr.log_softmax_fxp(x[:1024].clone(), b, f)
+        assert torch.equal(split, one[:1024]), (b, f)
+
+
+@pytest.mark.parametrize("cols,dtype,out_dtype,b,f", [
+    (32_768, torch.bfloat16, None, 32, 16),           # 2 spans of 2048 vectors
+    (40_000, torch.float16, torch.float32, 16, 8),    # 4 ragged spans
+    (128_256, torch.bfloat16, torch.float32, 64, 32),  # 8 spans, exact per-term path
+    (262_144, torch.bfloat16, None, 32, 16),          # 16 spans
+    (100_000, torch.float32, None, 64, 32),           # f32 rows, 16 ragged spans
+])
+def test_log_softmax_split_counts_bit_exact(cols, dtype, out_dtype, b, f):
+    x = _logits(3, cols, seed=cols % 97, dtype=dtype)
+    x[1, cols // 3] = 80.0  # the maximum inside one span: the others hold only small terms
+    got = torch.ops.fxpr.log_softmax_fxp(x.to(DEV), b, f, out_dtype).cpu()
+    want = from_np(R.log_softmax(to_np(x), IO_NAME[dtype], IO_NAME[out_dtype or dtype], b, f),
+                   out_dtype or dtype)
+    assert nan_aware_equal(got, want), mismatch_report(got, want)
+
+
+def test_log_softmax_split_concurrent_streams():
+    # every stream has its own sync region (16 per device; later streams take
+    # the one-workgroup kernel): concurrent calls on 20 streams, each checked
+    # against a serial call
+    xs = [_logits(8, 128_256, seed=40 + i).to(DEV) for i in range(20)]
+    want = [torch.ops.fxpr.log_softmax_fxp(x, 32, 16) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in xs]
+    outs = []
+    for _ in range(3):
+        for s, x in zip(streams, xs):
+            with torch.cuda.stream(s):
+                outs.append(torch.ops.fxpr.log_softmax_fxp(x, 32, 16))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert torch.equal(o, want[i % len(xs)]), i
+
+
 def test_log_softmax_batch_and_run_invariance():
     x = _logits(64, 128_256, seed=8).to(DEV)
     full = torch.ops.fxpr.log_softmax_fxp(x, 32, 16)

@@ -10,6 +10,9 @@
 // in registers between the reduction pass and the output pass so x is read
 // from HBM once.
 
+#include <atomic>
+#include <mutex>
+
 #include "rows_impl.h"
 
 namespace fxpr {
@@ -324,6 +327,255 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
   for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) emit(c, xr[c]);
 }
 
+// ---------------------------------------------------------------------------
+// Split log-softmax, for launches of few long rows. With one workgroup per
+// row a CU streams its row in, then computes (the maximum, the exp terms, two
+// workgroup reductions) with the memory idle, then streams the output. Here
+// 2^split_log2 workgroups (up to kSplitMax) share a row, each holding a
+// contiguous span of at most kSplitThreads * kSplitNreg 16-byte vectors in
+// registers: a CU runs eight spans at once, and the memory streams one
+// span's data while others compute. The workgroups of a row exchange their
+// span maxima, then their exact span sums (integers: the row's total, hence
+// every output bit, is the one-workgroup kernel's), through a sync region of
+// device memory, as tagged words: a 64-bit agent-scope atomic store of
+// (tag << 32 | 32-bit value), where the tag is the row's generation, one more
+// than the previous launch's. Wave 0 of every workgroup polls the row's words
+// (one lane per word, agent-scope atomic loads) until all carry the tag. A
+// word is written and read whole, so no ordering between different words is
+// needed, hence no fences. The generation is read at the start by every
+// workgroup of the row and advanced by span 0 once every span's sum is there
+// (every span has read it by then).
+// The host takes this kernel only when the whole grid fits on the GPU at once,
+// so no poll waits for a workgroup that cannot start; the poll is bounded
+// nonetheless (about a second), and a row whose wait gave up is written as
+// NaN.
+
+constexpr int kSplitMax = 16;        // workgroups per row, a power of two
+constexpr int kSplitRows = 1024;     // rows of one split launch
+constexpr int kSplitThreads = 256;
+constexpr int kSplitNreg = 8;        // 16-byte vectors per thread
+constexpr int kSplitMinVectors = 4096;  // shorter rows take the one-workgroup kernel
+constexpr int kSpinLimit = 1 << 20;
+
+struct LsmSync {
+  uint32_t generation[kSplitRows];
+  uint64_t maxima[kSplitRows][kSplitMax];     // tag | fp32 bit pattern
+  uint64_t sums[kSplitRows][kSplitMax * 4];   // tag | 32 bits of a span sum, low word first
+};
+
+// One region per stream that launched a split log-softmax, up to
+// kSyncRegions per device (later streams take the one-workgroup kernel).
+// Zero-initialised with the code object; calls on one stream are ordered, so
+// they never share a region at the same time.
+constexpr int kSyncRegions = 16;
+__device__ __align__(256) LsmSync lsm_sync[kSyncRegions];
+
+template <class U> __device__ __forceinline__ void store_agent(U* p, U v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class U> __device__ __forceinline__ U load_agent(U* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave 0: lane i < n polls words[i] until all n carry the tag; the lane's
+// 32-bit value in *val. False if the bounded poll gave up.
+__device__ __forceinline__ bool poll_tagged(uint64_t* words, int n, uint32_t tag, uint32_t* val) {
+  const int lane = threadIdx.x & 63;
+  uint64_t w = 0;
+  bool ok = false;
+  for (int it = 0; it < kSpinLimit; ++it) {
+    if (lane < n) w = load_agent(words + lane);
+    if (__builtin_amdgcn_ballot_w64(lane < n && uint32_t(w >> 32) != tag) == 0) {
+      ok = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  *val = uint32_t(w);
+  return ok;
+}
+
+// Eight waves per SIMD (at most 64 VGPRs): eight workgroups per CU.
+template <int XDT, int YDT, int VEC, int BITS, bool WIDE>
+__global__ __launch_bounds__(kSplitThreads, 8) void log_softmax_split_kernel(
+    const typename Io<XDT>::T* __restrict__ x, typename Io<YDT>::T* __restrict__ y, int64_t cols,
+    int frac, float inv_scale, int fast_sum, int split_log2, LsmSync* __restrict__ sync) {
+  using XV = Vec<typename Io<XDT>::T, VEC>;
+  using YV = Vec<typename Io<YDT>::T, VEC>;
+  using SumT = LseSum<WIDE>;
+  constexpr int NREG = kSplitNreg;
+  constexpr int NW = WIDE ? 4 : 2;  // 32-bit words of a span sum
+  __shared__ float fred[kSplitThreads / 64];
+  __shared__ SumT ired[kSplitThreads / 64];
+  __shared__ float row_max, row_lse_value;
+
+  const int split = 1 << split_log2;
+  const int row = static_cast<int>(blockIdx.x >> split_log2);
+  const int part = static_cast<int>(blockIdx.x & (split - 1));
+  const int64_t nchunks = cols / VEC;
+  const int64_t per = (nchunks + split - 1) >> split_log2;
+  const int64_t lo = part * per;
+  const int n = static_cast<int>(max<int64_t>(min<int64_t>(lo + per, nchunks) - lo, 0));
+  const int tid = threadIdx.x;
+  const bool wave0 = tid < 64;
+  const XV* xr = reinterpret_cast<const XV*>(x + int64_t(row) * cols) + lo;
+  YV* yr = reinterpret_cast<YV*>(y + int64_t(row) * cols) + lo;
+
+  // the row's tag (wave 0 only), read alongside the span
+  uint32_t tag = 0;
+  if (wave0) tag = load_agent(&sync->generation[row]) + 1;
+  XV keep[NREG];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    const int c = tid + i * kSplitThreads;
+    if (c < n) {
+      keep[i] = nt_load(xr + c);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) m = __builtin_elementwise_maximum(m, Io<XDT>::load(keep[i].v[j]));
+    }
+  }
+  m = block_max(m, fred);
+  if (wave0) {
+    if (tid == 0) store_agent(&sync->maxima[row][part], (uint64_t(tag) << 32) | __float_as_uint(m));
+    uint32_t v;
+    const bool ok = poll_tagged(sync->maxima[row], split, tag, &v);
+    float mm = tid < split ? __uint_as_float(v) : -__builtin_inff();
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mm = __builtin_elementwise_maximum(mm, __shfl_xor(mm, o, 64));
+    if (tid == 0) row_max = ok ? mm : __builtin_nanf("");
+  }
+  __syncthreads();
+  m = row_max;
+
+  SumT acc = 0;
+  if (BITS != 64 && fast_sum) {
+    const float zero_below = exp_zero_below(frac);
+    uint32_t acc32 = 0;
+#pragma unroll
+    for (int i = 0; i < NREG; ++i)
+      if (tid + i * kSplitThreads < n) add_terms_rc<XDT, VEC>(keep[i], m, frac, zero_below, acc32);
+    acc = acc32;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NREG; ++i)
+      if (tid + i * kSplitThreads < n) add_terms_exact<XDT, VEC, BITS>(keep[i], m, frac, acc);
+  }
+  if constexpr (VEC > 1) {
+#pragma unroll
+    for (int i = 0; i < NREG; ++i) asm volatile("" : "+v"(keep[i].v));
+  }
+  const SumT span_sum = block_exact_sum(acc, ired);
+  if (wave0) {
+    if (tid < NW)
+      store_agent(&sync->sums[row][part * NW + tid], (uint64_t(tag) << 32) | uint32_t(span_sum >> (32 * tid)));
+    uint32_t v;
+    const bool ok = poll_tagged(sync->sums[row], split * NW, tag, &v);
+    SumT total = tid < split * NW ? static_cast<SumT>(v) << (32 * (tid % NW)) : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      if constexpr (WIDE) total += shfl_xor_u128(total, o);
+      else total += __shfl_xor(total, o, 64);
+    }
+    if (tid == 0) {
+      row_lse_value = ok ? lse_of(m, total, inv_scale) : __builtin_nanf("");
+      if (part == 0) store_agent(&sync->generation[row], tag);
+    }
+  }
+  __syncthreads();
+  const float lse = row_lse_value;
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    const int c = tid + i * kSplitThreads;
+    if (c < n) {
+      YV yv;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) yv.v[j] = Io<YDT>::store(__fsub_rn(Io<XDT>::load(keep[i].v[j]), lse));
+      nt_store(yr + c, yv);
+    }
+  }
+}
+
+constexpr int kMaxDevices = 64;
+
+int stream_device(hipStream_t st, int* dev) {
+  hipError_t e = hipGetDevice(dev);
+  if (e == hipSuccess && st != nullptr) e = hipStreamGetDevice(st, dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  return (*dev < 0 || *dev >= kMaxDevices) ? FXPR_E_ARG : FXPR_OK;
+}
+
+std::mutex sync_mu;
+struct DeviceSync {
+  LsmSync* base = nullptr;
+  hipStream_t owner[kSyncRegions] = {};
+  int used = 0;
+};
+DeviceSync device_sync[kMaxDevices];
+
+// The stream's sync region, or nullptr: then the caller takes the
+// one-workgroup kernel. The device address of lsm_sync is looked up with the
+// device current, never while the stream is capturing.
+LsmSync* sync_region(hipStream_t st, int dev) {
+  std::lock_guard<std::mutex> lock(sync_mu);
+  DeviceSync& d = device_sync[dev];
+  if (d.base == nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(lsm_sync));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return nullptr;
+    d.base = static_cast<LsmSync*>(p);
+  }
+  for (int i = 0; i < d.used; ++i)
+    if (d.owner[i] == st) return d.base + i;
+  if (d.used == kSyncRegions) return nullptr;
+  d.owner[d.used] = st;
+  return d.base + d.used++;
+}
+
+// Workgroups of the kernel the device holds at once (cached per device).
+template <class K> int64_t resident_workgroups(K kernel, int dev) {
+  static std::atomic<int64_t> cache[kMaxDevices];
+  int64_t c = cache[dev].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kSplitThreads, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  c = int64_t(per_cu) * cus;
+  cache[dev].store(c, std::memory_order_relaxed);
+  return c;
+}
+
+// Launches the split kernel if the shape suits it; false: take the
+// one-workgroup kernel (nothing launched).
+template <int XDT, int YDT, int VEC, int BITS, bool WIDE>
+bool try_lsm_split(const void* x, void* y, int64_t rows, int64_t cols, int frac, hipStream_t st,
+                   int* rc) {
+  const int64_t nchunks = cols / VEC;
+  if (rows > kSplitRows || nchunks < kSplitMinVectors) return false;
+  int lg = 1;
+  while (lg < 4 && cdiv(nchunks, int64_t(1) << lg) > int64_t(kSplitThreads) * kSplitNreg) ++lg;
+  if (cdiv(nchunks, int64_t(1) << lg) > int64_t(kSplitThreads) * kSplitNreg) return false;
+  auto kernel = log_softmax_split_kernel<XDT, YDT, VEC, BITS, WIDE>;
+  int dev = 0;
+  if (stream_device(st, &dev) != FXPR_OK) return false;
+  if ((rows << lg) > resident_workgroups(kernel, dev)) return false;
+  LsmSync* sync = sync_region(st, dev);
+  if (sync == nullptr) return false;
+  const int fast = BITS != 64 && lse_fast_sum(BITS, frac, double(kSplitNreg) * VEC);
+  kernel<<<dim3(static_cast<unsigned>(rows << lg)), kSplitThreads, 0, st>>>(
+      static_cast<const typename Io<XDT>::T*>(x), static_cast<typename Io<YDT>::T*>(y), cols, frac,
+      pow2f(-frac), fast, lg, sync);
+  *rc = launch_status();
+  return true;
+}
+
 template <int XDT, int YDT, int VEC>
 int launch_lsm_vec(const void* x, void* y, int64_t rows, int64_t cols, int bits, int frac,
                    hipStream_t st) {
@@ -331,6 +583,15 @@ int launch_lsm_vec(const void* x, void* y, int64_t rows, int64_t cols, int bits,
   using YT = typename Io<YDT>::T;
   constexpr int NREG = VEC == 1 ? 8 : 32;
   const LseShape sh = lse_shape(cols, VEC, NREG, bits, frac);
+  // (128-bit sums, for near-flat rows at large f, keep the one-workgroup kernel)
+  if constexpr (VEC > 1) {
+    int rc = FXPR_OK;
+    bool done = false;
+    if (bits == 16) done = try_lsm_split<XDT, YDT, VEC, 16, false>(x, y, rows, cols, frac, st, &rc);
+    else if (bits == 32) done = try_lsm_split<XDT, YDT, VEC, 32, false>(x, y, rows, cols, frac, st, &rc);
+    else if (!sh.wide) done = try_lsm_split<XDT, YDT, VEC, 64, false>(x, y, rows, cols, frac, st, &rc);
+    if (done) return rc;
+  }
   const float inv = pow2f(-frac);
   dim3 grid(static_cast<unsigned>(rows));
   const XT* xp = static_cast<const XT*>(x);

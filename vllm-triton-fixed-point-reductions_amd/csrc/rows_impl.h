@@ -148,6 +148,42 @@ __device__ __forceinline__ float uint_to_f32(u128 v) {
 
 template <bool WIDE> using LseSum = typename std::conditional<WIDE, u128, uint64_t>::type;
 
+// Exact path: adds RNE_sat_b(exp_scaled(fl32(x_j) - m, f)) of one vector's
+// elements to acc. Branch-free (its thresholds, for large f, skip little).
+template <int XDT, int VEC, int BITS, class SumT>
+__device__ __forceinline__ void add_terms_exact(const Vec<typename Io<XDT>::T, VEC>& xv, float m, int frac,
+                                                SumT& acc) {
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
+    acc += static_cast<SumT>(quant_nonneg<BITS>(exp_scaled_to_round(d, frac)));
+  }
+}
+
+// Rounding-constant path (same terms): the wave computes an element slot's
+// exp only when some lane's difference reaches exp_zero_below (a uniform
+// branch: peaked rows skip most slots); the terms it skips are exactly 0.
+// The per-lane sum is a plain 32-bit add: the host enables this path only
+// when elements per lane x the largest term stay below 2^32.
+template <int XDT, int VEC>
+__device__ __forceinline__ void add_terms_rc(const Vec<typename Io<XDT>::T, VEC>& xv, float m, int frac,
+                                             float zero_below, uint32_t& acc32) {
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
+    if (__builtin_amdgcn_ballot_w64(d >= zero_below) != 0) {
+      const uint32_t q = exp_scaled_rc_bits(d, frac) - 0x4B400000u;
+      acc32 += d >= zero_below ? q : 0u;
+    }
+  }
+}
+
+// lse = m + ln(fl32(S) * 2^-f), -inf for S = 0 (so m + lse is NaN for a NaN m).
+template <class SumT> __device__ __forceinline__ float lse_of(float m, SumT total, float inv_scale) {
+  const float lnS = total == 0 ? -__builtin_inff() : log_own(__fmul_rn(uint_to_f32(total), inv_scale));
+  return __fadd_rn(m, lnS);
+}
+
 // The log-softmax reduction of one row, shared by every kernel that needs it.
 // m = max_j fl32(x_j) (IEEE maximum, NaN propagates: gfx950's
 // v_maximum3_f32; the sign of a zero maximum changes no output, as x - m and
@@ -156,10 +192,9 @@ template <bool WIDE> using LseSum = typename std::conditional<WIDE, u128, uint64
 // 2^-f) (-inf for S = 0). The thread's first NREG chunks (chunk c = tid +
 // i * blockDim.x) are left in keep[] in their storage type for the caller's
 // output pass; later chunks are re-read. fred / ired: kLsmThreads / 64
-// entries of shared memory. The per-lane sums of the rounding-constant path
-// (fast_sum) are plain 32-bit adds: the host enables it only when elements
-// per lane x the largest term stay below 2^32. WIDE (64-bit terms only)
-// takes 128-bit sums.
+// entries of shared memory. fast_sum selects the rounding-constant terms with
+// 32-bit lane sums (add_terms_rc). WIDE (64-bit terms only) takes 128-bit
+// sums.
 template <int XDT, int VEC, int NREG, int BITS, bool WIDE>
 __device__ __forceinline__ float row_lse(const Vec<typename Io<XDT>::T, VEC>* __restrict__ xr,
                                          Vec<typename Io<XDT>::T, VEC> (&keep)[NREG], int64_t nchunks,
@@ -187,46 +222,26 @@ __device__ __forceinline__ float row_lse(const Vec<typename Io<XDT>::T, VEC>* __
   }
   m = block_max(m, fred);
 
-  // On the rounding-constant path the wave computes an element slot's exp
-  // only when some lane's difference reaches exp_zero_below (a uniform
-  // branch: peaked rows skip most slots); the terms it skips are exactly 0.
-  // The exact path stays branch-free (its thresholds, for large f, skip
-  // little).
-  const float zero_below = exp_zero_below(frac);
   SumT acc = 0;
-  auto accum = [&](const XV& xv) {
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
-      acc += static_cast<SumT>(quant_nonneg<BITS>(exp_scaled_to_round(d, frac)));
-    }
-  };
   if (BITS != 64 && fast_sum) {
+    const float zero_below = exp_zero_below(frac);
     uint32_t acc32 = 0;
-    auto accum_rc = [&](const XV& xv) {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const float d = __fsub_rn(Io<XDT>::load(xv.v[j]), m);
-        if (__builtin_amdgcn_ballot_w64(d >= zero_below) != 0) {
-          const uint32_t q = exp_scaled_rc_bits(d, frac) - 0x4B400000u;
-          acc32 += d >= zero_below ? q : 0u;
-        }
-      }
-    };
 #pragma unroll
     for (int i = 0; i < NREG; ++i) {
       const int64_t c = tid + static_cast<int64_t>(i) * nthr;
-      if (c < nchunks) accum_rc(keep[i]);
+      if (c < nchunks) add_terms_rc<XDT, VEC>(keep[i], m, frac, zero_below, acc32);
     }
-    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum_rc(xr[c]);
+    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr)
+      add_terms_rc<XDT, VEC>(xr[c], m, frac, zero_below, acc32);
     acc = acc32;
   } else {
 #pragma unroll
     for (int i = 0; i < NREG; ++i) {
       const int64_t c = tid + static_cast<int64_t>(i) * nthr;
-      if (c < nchunks) accum(keep[i]);
+      if (c < nchunks) add_terms_exact<XDT, VEC, BITS>(keep[i], m, frac, acc);
     }
-    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) accum(xr[c]);
+    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr)
+      add_terms_exact<XDT, VEC, BITS>(xr[c], m, frac, acc);
   }
   // The row stays in registers in its storage type: an empty asm "changing"
   // it keeps the compiler from holding every element's fp32 widening (twice
@@ -235,9 +250,7 @@ __device__ __forceinline__ float row_lse(const Vec<typename Io<XDT>::T, VEC>* __
 #pragma unroll
     for (int i = 0; i < NREG; ++i) asm volatile("" : "+v"(keep[i].v));
   }
-  const SumT total = block_exact_sum(acc, ired);
-  const float lnS = total == 0 ? -__builtin_inff() : log_own(__fmul_rn(uint_to_f32(total), inv_scale));
-  return __fadd_rn(m, lnS);
+  return lse_of(m, block_exact_sum(acc, ired), inv_scale);
 }
 
 // Host side: workgroup size and sum path of a row_lse launch.
@@ -247,17 +260,22 @@ struct LseShape {
   bool wide;      // 128-bit sums
 };
 
+// Whether lanes of lane_elems elements may take the rounding-constant terms
+// with 32-bit lane sums: 1.4143 * 2^f below 2^22 and qmax, and a lane's terms
+// summing below 2^32.
+inline bool lse_fast_sum(int bits, int frac, double lane_elems) {
+  const double qmax = double(qmax_for_bits(bits));
+  // the largest term: e^0 * 2^f, with margin for the polynomial, or qmax
+  const double term_max = std::fmin(1.4143 * std::ldexp(1.0, frac) + 1.0, qmax);
+  return bits != 64 && term_max < 4194304.0 && term_max < qmax && lane_elems * term_max < 4294967296.0;
+}
+
 inline LseShape lse_shape(int64_t cols, int vec, int nreg, int bits, int frac) {
   LseShape s;
   const int64_t nchunks = cols / vec;
   s.threads = threads_for(nchunks, nreg, kLsmThreads);
-  const double qmax = double(qmax_for_bits(bits));
-  // the largest term: e^0 * 2^f, with margin for the polynomial, or qmax
-  const double term_max = std::fmin(1.4143 * std::ldexp(1.0, frac) + 1.0, qmax);
-  // rounding-constant sums: 1.4143 * 2^f below 2^22 and qmax, and a lane's
-  // terms summing below 2^32
-  const double lane_elems = double(cdiv(nchunks, s.threads)) * vec;
-  s.fast_sum = bits != 64 && term_max < 4194304.0 && term_max < qmax && lane_elems * term_max < 4294967296.0;
+  const double term_max = std::fmin(1.4143 * std::ldexp(1.0, frac) + 1.0, double(qmax_for_bits(bits)));
+  s.fast_sum = lse_fast_sum(bits, frac, double(cdiv(nchunks, s.threads)) * vec);
   s.wide = double(cols) * term_max >= 18446744073709551616.0;
   return s;
 }
