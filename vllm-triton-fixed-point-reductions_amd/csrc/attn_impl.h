@@ -1477,10 +1477,19 @@ template <int DMAX> struct PDmaGeom {
   static constexpr int NDMA = RPW / KPI;             // DMA instructions per wave per tile
   static constexpr int NS = 4;                       // LDS stages (two workgroups per CU)
   static_assert(NDMA >= 1 && NDMA * KPI == RPW, "tile rows per wave");
+  // K tiles: the transposed score MFMAs read rows {0-3, 8-11, 16-19, 24-27}
+  // (and the same + 4) of a 32-row group in one 16-lane read, so the row
+  // swizzle takes row bits 0-1 and 3-4 (injective on each such set: distinct
+  // 16-byte bank groups). 128-byte rows: a 256-byte bank window holds a row
+  // pair, and bits 1, 3, 4 spread each parity class.
+  static __device__ __forceinline__ int kswz(int r) {
+    if constexpr (CPR >= 16) return ((r & 3) << 2) | ((r >> 3) & 3);
+    else return ((r >> 1) & 1) | (((r >> 3) & 3) << 1);
+  }
 };
 
 template <int DMAX> constexpr size_t prefill_dma_lds_bytes() {
-  return size_t(PDmaGeom<DMAX>::NS) * PDmaGeom<DMAX>::TILEB + size_t(PQ_WAVES) * 16 * (TILE + 8) * 2;
+  return size_t(PDmaGeom<DMAX>::NS) * PDmaGeom<DMAX>::TILEB;
 }
 
 __device__ __forceinline__ void lds_write_b16_hi(unsigned addr, uint32_t x) {
@@ -1526,9 +1535,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   constexpr int QSTEPS = DMAX / KI;
   constexpr int DBLK = DMAX / 16;
   constexpr int NK0 = QUNIT / KI;  // MFMA k steps per quantised chain
-  constexpr int VP = TILE + 8;     // Ps row pitch (elements)
   constexpr int NS = G::NS;
-  constexpr int PS_OFF = NS * G::TILEB;
   static_assert(TILE == QUNIT, "one quantised chain per tile");
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(smem_raw));
@@ -1571,23 +1578,35 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     const int lb = __builtin_amdgcn_readfirstlane(key0 >> a.ps_shift);
     return bt_row[min(lb, a.max_blocks - 1)];
   };
-  auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
+  // K and V tiles are separate compile-time instances behind a uniform
+  // branch on isv (a select between the two matrices' fields becomes a load
+  // through a selected address, which keeps the captured values in scratch
+  // memory, reloaded at every DMA; those reloads' vmcnt waits drain the ring).
+  auto dma_mat = [&](auto isv_tag, int t, int ent, int buf) __attribute__((always_inline)) {
+    constexpr bool ISV = decltype(isv_tag)::value;
     const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
+    const uint32_t sb = uint32_t(ISV ? a.sv_b : a.sk_b), ss = uint32_t(ISV ? a.sv_s : a.sk_s),
+                   sh = uint32_t(ISV ? a.sv_h : a.sk_h);
 #pragma unroll
     for (int q = 0; q < G::NDMA; ++q) {
       const int row0q = G::RPW * wave + q * G::KPI;
       const int rr = row0q + lane / G::CPR;
       const int key = min(t * TILE + rr, seq_len - 1);
-      const int c = (lane % G::CPR) ^ SW::swz(rr);
-      const int64_t sb = isv ? a.sv_b : a.sk_b, ss = isv ? a.sv_s : a.sk_s, sh = isv ? a.sv_h : a.sk_h;
-      const uint64_t off = uint64_t(p) * uint32_t(sb) + uint64_t(uint32_t(key & (a.page_size - 1))) * uint32_t(ss) +
-                           uint64_t(uint32_t(g)) * uint32_t(sh) + uint32_t(c * 8);
-      const T* src = (isv ? Vc : Kc) + off;
+      const int c = (lane % G::CPR) ^ (ISV ? SW::swz(rr) : G::kswz(rr));
+      const uint64_t off = uint64_t(p) * sb + uint64_t(uint32_t(key & (a.page_size - 1))) * ss +
+                           uint64_t(uint32_t(g)) * sh + uint32_t(c * 8);
+      const T* src = (ISV ? Vc : Kc) + off;
       const unsigned dst = lds0 + buf * G::TILEB + row0q * G::ROWB;
       // (temporal: a workgroup reads each K tile twice and neighbouring
       // row blocks share tiles through L2; nt measured 5 % slower)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
     }
+  };
+  auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
+    if (isv)
+      dma_mat(std::true_type{}, t, ent, buf);
+    else
+      dma_mat(std::false_type{}, t, ent, buf);
   };
 
   // The tile stream: per chunk cc, its nt live K tiles (phase 0), then K and
@@ -1625,44 +1644,51 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     }
   }
 
-  // Q fragments of the wave's rows (MFMA A operand: row lane%16, k slots kg).
+  // The lane's query row. Scores and weighted V are computed transposed:
+  // MFMA (s, h) of a tile (s: 32-key step, h: half) takes the key rows
+  // pi(i) = 32 s + 8 (i / 4) + 4 h + i % 4 (i = lane % 16) of the K tile as
+  // its A operand and the wave's Q rows as its B operand, so lane (kg, row
+  // lane % 16) receives the scores of keys 32 s + 8 kg + 4 h + e, e = 0..3;
+  // with h = 0, 1 these are the eight consecutive keys 32 s + 8 kg .. + 7 that
+  // the weighted-V MFMA (V^T as A operand, P^T as B operand) needs in that
+  // lane's B operand, so the weights never leave registers, and every
+  // statistic of a row (maximum, denominator, fold) lives in the row's four
+  // lanes. The MFMA is bitwise symmetric in its operands and each score and
+  // weighted-V element is the same products in the same k order as in the
+  // untransposed layout, so every bit is attn_dma_kernel's.
+  const RowInfo me = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + (lane & 15));
   u32x4 qf[QSTEPS];
   {
-    const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + (lane & 15));
-    const T* qbase = static_cast<const T*>(a.q) + qrow.token * a.sq_t + int64_t(qrow.head) * a.sq_h;
+    const T* qbase = static_cast<const T*>(a.q) + me.token * a.sq_t + int64_t(me.head) * a.sq_h;
 #pragma unroll
     for (int j = 0; j < QSTEPS; ++j) {
       const int d = 32 * j + 8 * kg;
-      qf[j] = qrow.valid ? *reinterpret_cast<const u32x4*>(qbase + d) : u32x4{0u, 0u, 0u, 0u};
+      qf[j] = me.valid ? *reinterpret_cast<const u32x4*>(qbase + d) : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  // Rows of the score / PV layout: the wave's rows 4*kg + e.
-  int ks[4], ke[4], qp[4];
-  float slope[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + 4 * kg + e);
-    ks[e] = ri.valid ? ri.kstart : 0x7fffffff;
-    ke[e] = ri.valid ? ri.kend : 0;
-    qp[e] = ri.qpos;
-    slope[e] = a.alibi ? a.alibi[ri.head] : 0.0f;
-  }
+  const int ks = me.valid ? me.kstart : 0x7fffffff;
+  const int ke = me.valid ? me.kend : 0;
+  const int qp = me.qpos;
+  const float slope = a.alibi ? a.alibi[me.head] : 0.0f;
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): Q, row setup and the first DMAs
 
-  // Per-lane LDS offsets within a stage. K fragment j of key row kb*16 +
-  // lane%16: chunk 4j + kg (the swizzle depends on the row's low four bits
-  // only, so key block kb adds kb * 16 rows). V B-operand reads
-  // (ds_read_b64_tr_b16) of d block db: keys s*KI + 8kg + (j>>2) (+4 for the
-  // upper half), columns db*16 + 4*(j&3), j = lane%16: chunk 2 db + b of row
-  // rr sits at slot (2 db + b) ^ swz(rr) = 2 db ^ (b ^ swz(rr)), i.e. at the
-  // d block 0 offset XOR db << 5 (bits 5.. of the chunk part; the row and
-  // half-chunk parts lie outside them).
-  unsigned koff[QSTEPS];
+  // Per-lane LDS offsets within a stage. K A-operand rows pi(i) for h = 0, 1
+  // (the step s adds 32 rows, which the K swizzle ignores): chunk 4 j + kg at
+  // slot (4 j + kg) ^ kswz(row). V A-operand reads (ds_read_b64_tr_b16) of d
+  // block db: keys s*KI + 8kg + (j>>2) (+4 for the upper half), columns
+  // db*16 + 4*(j&3), j = lane%16: chunk 2 db + b of row rr sits at slot
+  // (2 db + b) ^ swz(rr) = 2 db ^ (b ^ swz(rr)), i.e. at the d block 0 offset
+  // XOR db << 5 (bits 5.. of the chunk part; the row and half-chunk parts lie
+  // outside them).
+  unsigned koff[2][QSTEPS];
 #pragma unroll
-  for (int j = 0; j < QSTEPS; ++j) {
-    const int rr = lane & 15;
-    koff[j] = rr * G::ROWB + (((4 * j + kg) ^ SW::swz(rr)) << 4);
-  }
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) {
+      const int i = lane & 15;
+      const int rr = 8 * (i >> 2) + 4 * h + (i & 3);
+      koff[h][j] = rr * G::ROWB + (((4 * j + kg) ^ G::kswz(rr)) << 4);
+    }
   unsigned voff0[NK0][2];
 #pragma unroll
   for (int s = 0; s < NK0; ++s)
@@ -1672,10 +1698,9 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       const int rr = s * KI + 8 * kg + (j >> 2) + 4 * h;
       voff0[s][h] = rr * G::ROWB + ((((j & 3) >> 1) ^ SW::swz(rr)) << 4) + (j & 1) * 8;
     }
-  const unsigned ps_w = lds0 + PS_OFF + wave * 16 * VP * 2;  // the wave's P [16][VP]
 
-  float Mr[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
-  AccT Dr[4] = {0, 0, 0, 0};
+  float Mr = -__builtin_inff();
+  AccT Dr = 0;
   AccT Wr[DBLK][4];
 #pragma unroll
   for (int b = 0; b < DBLK; ++b)
@@ -1686,7 +1711,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   // score is fl(acc * scale) and the chunk maximum is fl(max(acc) * scale)
   // (rounding is monotone); tiles every row of the wave sees whole skip the
   // mask; a weight w in [0, 1] quantises by the rounding constant (2^f within
-  // its range, see fast_den); P is stored without the canonical-NaN rule (any
+  // its range, see fast_den); P is packed without the canonical-NaN rule (any
   // NaN weight yields a NaN weighted V either way, which quantises to 0).
   const bool fast_den = BITS != 64 && a.fxp_scale <= (BITS == 16 ? 16384.0f : 4194304.0f);
   const bool fast = fast_den && !(a.softcap_log2 > 0.0f) && !a.alibi && a.scale_log2 > 0.0f;
@@ -1715,26 +1740,25 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       return e;
     };
     auto stage_base = [&](int e) -> unsigned { return lds0 + (e % NS) * G::TILEB; };
-    // The key blocks of the tile at base, software-pipelined: block kb + 1's
-    // fragment reads are issued before block kb's MFMA chain (attn_kernel's
-    // chain per score) and fn(kb, acc); fn may issue LDS writes, which the
-    // next wait covers too (LDS operations complete in order; only the newest
-    // block's QSTEPS reads may remain in flight).
-    auto key_blocks = [&](unsigned base, auto&& fn) __attribute__((always_inline)) {
+    // The four transposed score MFMA chains of the tile at base (q = 2 s + h),
+    // software-pipelined: chain q + 1's fragment reads are issued before chain
+    // q's wait, MFMAs and fn(q, acc) (only the newest chain's QSTEPS reads may
+    // remain in flight at the wait).
+    auto key_groups = [&](unsigned base, auto&& fn) __attribute__((always_inline)) {
       u32x4 kf[2][QSTEPS];
-      auto issue = [&](auto kbc) __attribute__((always_inline)) {
-        constexpr int kb = decltype(kbc)::value;
+      auto issue = [&](auto qc) __attribute__((always_inline)) {
+        constexpr int q = decltype(qc)::value;
         static_for<QSTEPS>([&](auto jc) {
           constexpr int j = decltype(jc)::value;
-          lds_read_b128_off<kb * 16 * G::ROWB>(base + koff[j], kf[kb & 1][j]);
+          lds_read_b128_off<(q >> 1) * 32 * G::ROWB>(base + koff[q & 1][j], kf[q & 1][j]);
         });
       };
       issue(std::integral_constant<int, 0>{});
-      static_for<TILE / 16>([&](auto kbc) {
-        constexpr int kb = decltype(kbc)::value;
-        u32x4(&cur)[QSTEPS] = kf[kb & 1];
-        if constexpr (kb + 1 < TILE / 16) {
-          issue(std::integral_constant<int, kb + 1>{});
+      static_for<4>([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        u32x4(&cur)[QSTEPS] = kf[q & 1];
+        if constexpr (q + 1 < 4) {
+          issue(std::integral_constant<int, q + 1>{});
           if constexpr (QSTEPS == 4) lds_waitn_for<QSTEPS>(cur[0], cur[1], cur[2], cur[3]);
           else lds_waitn_for<QSTEPS>(cur[0], cur[1]);
         } else {
@@ -1743,63 +1767,54 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
         }
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < QSTEPS; ++j) acc = TR::mma(qf[j], cur[j], acc);
-        fn(kbc, acc);
+        for (int j = 0; j < QSTEPS; ++j) acc = TR::mma(cur[j], qf[j], acc);
+        fn(qc, acc);
         __builtin_amdgcn_sched_barrier(0);
       });
     };
-    // Scores of key block kb of tile t for the lane's rows (attn_kernel's
-    // post-processing); whole: every row of the wave sees the whole tile.
-    auto block_scores = [&](const f32x4& acc, int t, int kb, bool whole, float (&sc)[4]) __attribute__((always_inline)) {
-      const int key = t * TILE + kb * 16 + (lane & 15);
+    // Scores of chain q of tile t for the lane's row and keys
+    // t * TILE + 32 (q >> 1) + 8 kg + 4 (q & 1) + e; whole: the wave's rows see
+    // the whole tile.
+    auto chain_scores = [&](const f32x4& acc, int t, int q, bool whole, float (&sc)[4]) __attribute__((always_inline)) {
+      const int key0 = t * TILE + 32 * (q >> 1) + 8 * kg + 4 * (q & 1);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float x = __fmul_rn(acc[e], a.scale_log2);
         if constexpr (!FAST) {
           if (a.softcap_log2 > 0.0f) x = a.softcap_log2 * tanh_approx(x / a.softcap_log2);
-          if (a.alibi) x = x + slope[e] * static_cast<float>(key - qp[e]);
+          if (a.alibi) x = x + slope * static_cast<float>(key0 + e - qp);
         }
-        sc[e] = (whole || (key >= ks[e] && key < ke[e])) ? x : -__builtin_inff();
+        sc[e] = (whole || (key0 + e >= ks && key0 + e < ke)) ? x : -__builtin_inff();
       }
     };
     auto tile_whole = [&](int t) -> bool {
-      bool out = false;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) out = out || !(ks[e] <= t * TILE && t * TILE + TILE <= ke[e]);
-      return __builtin_amdgcn_ballot_w64(out) == 0;
+      return __builtin_amdgcn_ballot_w64(!(ks <= t * TILE && t * TILE + TILE <= ke)) == 0;
     };
 
     for (int c = c_lo; c < c_hi; ++c) {
       const int ta = live_lo(c), te = live_hi(c);
-      float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
-      float mraw[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+      float mx = -__builtin_inff(), mraw = -__builtin_inff();
       // phase 0: the chunk's row maxima
       for (int t = ta; t < te; ++t) {
         const unsigned base = stage_base(step_begin(std::integral_constant<int, 1>{}));
         if (FAST && tile_whole(t)) {
-          key_blocks(base, [&](auto, const f32x4& acc) __attribute__((always_inline)) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) mraw[e] = fmaxf(mraw[e], acc[e]);
+          key_groups(base, [&](auto, const f32x4& acc) __attribute__((always_inline)) {
+            mraw = fmaxf(fmaxf(mraw, fmaxf(acc[0], acc[1])), fmaxf(acc[2], acc[3]));
           });
         } else {
-          key_blocks(base, [&](auto kbc, const f32x4& acc) __attribute__((always_inline)) {
+          key_groups(base, [&](auto qc, const f32x4& acc) __attribute__((always_inline)) {
             float sc[4];
-            block_scores(acc, t, decltype(kbc)::value, false, sc);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], sc[e]);
+            chain_scores(acc, t, decltype(qc)::value, false, sc);
+            mx = fmaxf(fmaxf(mx, fmaxf(sc[0], sc[1])), fmaxf(sc[2], sc[3]));
           });
         }
       }
-      float m[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (FAST) mx[e] = fmaxf(mx[e], __fmul_rn(mraw[e], a.scale_log2));
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], o, 64));
-        m[e] = mx[e] != -__builtin_inff() ? mx[e] : 0.0f;  // no key: pin to 0
-      }
+      if constexpr (FAST) mx = fmaxf(mx, __fmul_rn(mraw, a.scale_log2));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m = mx != -__builtin_inff() ? mx : 0.0f;  // no key: pin to 0
       // phase 1: weights and weighted V, tile by tile
-      AccT den[4] = {0, 0, 0, 0};
+      AccT den = 0;
       AccT wv[DBLK][4];
 #pragma unroll
       for (int b = 0; b < DBLK; ++b)
@@ -1807,52 +1822,51 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
         for (int e = 0; e < 4; ++e) wv[b][e] = 0;
       for (int t = ta; t < te; ++t) {
         const int e = step_begin(std::integral_constant<int, 2>{});  // K(t), then V(t)
+        // P^T B operands of the two 32-key steps: word 2 h + e / 2 of pb[s]
+        // holds the weights of keys 32 s + 8 kg + 4 h + e
+        u32x4 pb[NK0];
         {
           const unsigned base = stage_base(e);
-          auto weights = [&](bool whole) __attribute__((always_inline)) {
-            key_blocks(base, [&](auto kbc, const f32x4& acc) __attribute__((always_inline)) {
-              constexpr int kb = decltype(kbc)::value;
+          // (whole as a type: two calls of one closure type would be merged
+          // into one body whose closure references live in scratch memory)
+          auto weights = [&](auto whole_tag) __attribute__((always_inline)) {
+            constexpr bool WHOLE = decltype(whole_tag)::value;
+            key_groups(base, [&](auto qc, const f32x4& acc) __attribute__((always_inline)) {
+              constexpr int q = decltype(qc)::value, s = q >> 1, h = q & 1;
               float sc[4];
-              block_scores(acc, t, kb, whole, sc);
+              chain_scores(acc, t, q, WHOLE, sc);
               float w[4];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) w[e] = __builtin_amdgcn_exp2f(sc[e] - m[e]);
-              const unsigned pw = ps_w + ((4 * kg) * VP + kb * 16 + (lane & 15)) * 2;
+              for (int i = 0; i < 4; ++i) w[i] = __builtin_amdgcn_exp2f(sc[i] - m);
               if constexpr (FAST) {
                 // w * 2^f + 1.5 * 2^23 (exact product, one rounding: RNE) has
                 // the bits of RNE(w * 2^f) + 0x4B400000; NaN -> the constant
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  const float y = fmaxf(__builtin_fmaf(w[e], a.fxp_scale, 12582912.0f), 12582912.0f);
-                  den[e] = static_cast<int32_t>(static_cast<uint32_t>(den[e]) + __float_as_uint(y) - 0x4B400000u);
+                for (int i = 0; i < 4; ++i) {
+                  const float y = fmaxf(__builtin_fmaf(w[i], a.fxp_scale, 12582912.0f), 12582912.0f);
+                  den = static_cast<int32_t>(static_cast<uint32_t>(den) + __float_as_uint(y) - 0x4B400000u);
                 }
-#pragma unroll
-                for (int e = 0; e < 4; e += 2) {
-                  const uint32_t pk = p_pack2<DT>(w[e], w[e + 1]);
-                  lds_write_b16(pw + e * VP * 2, pk);
-                  lds_write_b16_hi(pw + (e + 1) * VP * 2, pk);
-                }
+                pb[s][2 * h] = p_pack2<DT>(w[0], w[1]);
+                pb[s][2 * h + 1] = p_pack2<DT>(w[2], w[3]);
               } else {
+                uint32_t p16[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  den[e] = wadd<BITS>(den[e], quant<BITS>(__fmul_rn(w[e], a.fxp_scale)));
-                  lds_write_b16(pw + e * VP * 2, Io<DT>::store(w[e]));
+                for (int i = 0; i < 4; ++i) {
+                  den = wadd<BITS>(den, quant<BITS>(__fmul_rn(w[i], a.fxp_scale)));
+                  p16[i] = Io<DT>::store(w[i]);
                 }
+                pb[s][2 * h] = p16[0] | (p16[1] << 16);
+                pb[s][2 * h + 1] = p16[2] | (p16[3] << 16);
               }
             });
           };
           if (FAST && tile_whole(t))
-            weights(true);
+            weights(std::true_type{});
           else
-            weights(false);
+            weights(std::false_type{});
         }
         {
-          // the wave's own P writes complete before its reads
-          lds_wait();
           const unsigned base = stage_base(e + 1);
-          u32x4 pa[NK0];
-#pragma unroll
-          for (int s = 0; s < NK0; ++s) lds_read_b128(ps_w + ((lane & 15) * VP + s * KI + 8 * kg) * 2, pa[s]);
           // d blocks software-pipelined: block db + 1's V reads go out before
           // block db's wait (only they may remain in flight)
           uint64_t vr[2][NK0][2];
@@ -1875,35 +1889,32 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
               if constexpr (NK0 == 2) lds_wait_for(cur[0][0], cur[0][1], cur[1][0], cur[1][1]);
               else lds_wait_for(cur[0][0], cur[0][1]);
             }
-            if constexpr (db == 0) {
-              if constexpr (NK0 == 2) lds_wait_for(pa[0], pa[1]);  // already complete: binds the registers
-              else lds_wait_for(pa[0]);
-            }
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NK0; ++s) {
               const u32x4 vb = {uint32_t(cur[s][0]), uint32_t(cur[s][0] >> 32), uint32_t(cur[s][1]),
                                 uint32_t(cur[s][1] >> 32)};
-              acc = TR::mma(pa[s], vb, acc);
+              acc = TR::mma(vb, pb[s], acc);
             }
+            // lane: d = 16 db + 4 kg + e of its row
 #pragma unroll
-            for (int e = 0; e < 4; ++e) wv[db][e] = wadd<BITS>(wv[db][e], quant<BITS>(__fmul_rn(acc[e], a.fxp_scale)));
+            for (int i = 0; i < 4; ++i) wv[db][i] = wadd<BITS>(wv[db][i], quant<BITS>(__fmul_rn(acc[i], a.fxp_scale)));
             __builtin_amdgcn_sched_barrier(0);
           });
         }
       }
-      // the chunk's denominators over the 16 key lanes, then the fold
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) den[e] = wadd<BITS>(den[e], __shfl_xor(den[e], o, 64));
-        if (mx[e] == -__builtin_inff()) continue;  // no key of the row in this chunk
+      // the chunk's denominator over the row's four lanes, then the fold
+      den = wadd<BITS>(den, __shfl_xor(den, 16, 64));
+      den = wadd<BITS>(den, __shfl_xor(den, 32, 64));
+      if (mx != -__builtin_inff()) {  // else no key of the row in this chunk
         float Mn, fa, fb;
-        merge_factors(Mr[e], mx[e], Mn, fa, fb);
-        Dr[e] = wadd<BITS>(rescale<BITS>(Dr[e], fa), rescale<BITS>(den[e], fb));
+        merge_factors(Mr, mx, Mn, fa, fb);
+        Dr = wadd<BITS>(rescale<BITS>(Dr, fa), rescale<BITS>(den, fb));
 #pragma unroll
-        for (int b = 0; b < DBLK; ++b) Wr[b][e] = wadd<BITS>(rescale<BITS>(Wr[b][e], fa), rescale<BITS>(wv[b][e], fb));
-        Mr[e] = Mn;
+        for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Wr[b][i] = wadd<BITS>(rescale<BITS>(Wr[b][i], fa), rescale<BITS>(wv[b][i], fb));
+        Mr = Mn;
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // DMAs into unused stages
@@ -1919,20 +1930,13 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     }
   }
 
-  float den_f[4];
+  if (me.valid) {
+    const float den_f = fmaxf(acc_f32<BITS>(Dr, a.fxp_inv), 1.0e-6f);
+    T* orow = static_cast<T*>(a.o) + me.token * a.so_t + int64_t(me.head) * a.so_h;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) den_f[e] = fmaxf(acc_f32<BITS>(Dr[e], a.fxp_inv), 1.0e-6f);
-  T* Op = static_cast<T*>(a.o);
+    for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-  for (int b = 0; b < DBLK; ++b) {
-    const int d = b * 16 + (lane & 15);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, wrow0 + 4 * kg + e);
-      if (!ri.valid) continue;
-      Op[ri.token * a.so_t + int64_t(ri.head) * a.so_h + d] =
-          Io<DT>::store(div_rn(acc_f32<BITS>(Wr[b][e], a.fxp_inv), den_f[e]));
-    }
+      for (int i = 0; i < 4; ++i) orow[b * 16 + 4 * kg + i] = Io<DT>::store(div_rn(acc_f32<BITS>(Wr[b][i], a.fxp_inv), den_f));
   }
 }
 
