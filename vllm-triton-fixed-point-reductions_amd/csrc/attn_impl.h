@@ -1478,12 +1478,12 @@ template <int DMAX> struct PDmaGeom {
   static constexpr int NS = 4;                       // LDS stages (two workgroups per CU)
   static_assert(NDMA >= 1 && NDMA * KPI == RPW, "tile rows per wave");
   // K tiles: the transposed score MFMAs read rows {0-3, 8-11, 16-19, 24-27}
-  // (and the same + 4) of a 32-row group in one 16-lane read, so the row
-  // swizzle takes row bits 0-1 and 3-4 (injective on each such set: distinct
-  // 16-byte bank groups). 128-byte rows: a 256-byte bank window holds a row
-  // pair, and bits 1, 3, 4 spread each parity class.
+  // (and the same + 4) of a 32-row group in one 16-lane read. Measured with
+  // gfx950's LDS conflict counter on that exact pattern: 256-byte rows keep
+  // the V swizzle (conflict-free; the alternatives tried were 2-way),
+  // 128-byte rows take row bits 1, 3 and 4 (the V swizzle there is 2-way).
   static __device__ __forceinline__ int kswz(int r) {
-    if constexpr (CPR >= 16) return ((r & 3) << 2) | ((r >> 3) & 3);
+    if constexpr (CPR >= 16) return DmaGeom<DMAX>::swz(r);
     else return ((r >> 1) & 1) | (((r >> 3) & 3) << 1);
   }
 };
@@ -1582,21 +1582,29 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   // branch on isv (a select between the two matrices' fields becomes a load
   // through a selected address, which keeps the captured values in scratch
   // memory, reloaded at every DMA; those reloads' vmcnt waits drain the ring).
+  // Per-lane parts of the DMA sources, fixed for the kernel: the row of the
+  // wave's instruction q and its chunk offset under the K and V swizzles.
+  int dma_rr[G::NDMA];
+  uint32_t dma_ck[G::NDMA], dma_cv[G::NDMA];
+#pragma unroll
+  for (int q = 0; q < G::NDMA; ++q) {
+    const int rr = G::RPW * wave + q * G::KPI + lane / G::CPR;
+    dma_rr[q] = rr;
+    dma_ck[q] = uint32_t(((lane % G::CPR) ^ G::kswz(rr)) * 8);
+    dma_cv[q] = uint32_t(((lane % G::CPR) ^ SW::swz(rr)) * 8);
+  }
   auto dma_mat = [&](auto isv_tag, int t, int ent, int buf) __attribute__((always_inline)) {
     constexpr bool ISV = decltype(isv_tag)::value;
     const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
-    const uint32_t sb = uint32_t(ISV ? a.sv_b : a.sk_b), ss = uint32_t(ISV ? a.sv_s : a.sk_s),
-                   sh = uint32_t(ISV ? a.sv_h : a.sk_h);
+    const uint32_t ss = uint32_t(ISV ? a.sv_s : a.sk_s);
+    // the page's (and head's) first element, uniform
+    const T* base = (ISV ? Vc : Kc) + (uint64_t(p) * uint32_t(ISV ? a.sv_b : a.sk_b) +
+                                       uint64_t(uint32_t(g)) * uint32_t(ISV ? a.sv_h : a.sk_h));
 #pragma unroll
     for (int q = 0; q < G::NDMA; ++q) {
-      const int row0q = G::RPW * wave + q * G::KPI;
-      const int rr = row0q + lane / G::CPR;
-      const int key = min(t * TILE + rr, seq_len - 1);
-      const int c = (lane % G::CPR) ^ (ISV ? SW::swz(rr) : G::kswz(rr));
-      const uint64_t off = uint64_t(p) * sb + uint64_t(uint32_t(key & (a.page_size - 1))) * ss +
-                           uint64_t(uint32_t(g)) * sh + uint32_t(c * 8);
-      const T* src = (ISV ? Vc : Kc) + off;
-      const unsigned dst = lds0 + buf * G::TILEB + row0q * G::ROWB;
+      const int key = min(t * TILE + dma_rr[q], seq_len - 1);
+      const T* src = base + (uint64_t(uint32_t(key & (a.page_size - 1))) * ss + (ISV ? dma_cv[q] : dma_ck[q]));
+      const unsigned dst = lds0 + buf * G::TILEB + (G::RPW * wave + q * G::KPI) * G::ROWB;
       // (temporal: a workgroup reads each K tile twice and neighbouring
       // row blocks share tiles through L2; nt measured 5 % slower)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
@@ -1715,6 +1723,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   // NaN weight yields a NaN weighted V either way, which quantises to 0).
   const bool fast_den = BITS != 64 && a.fxp_scale <= (BITS == 16 ? 16384.0f : 4194304.0f);
   const bool fast = fast_den && !(a.softcap_log2 > 0.0f) && !a.alibi && a.scale_log2 > 0.0f;
+  const float vlim = (BITS == 16 ? 32767.0f : 4194304.0f) / a.fxp_scale;  // 2^f: exact
   auto run = [&](auto fast_tag) __attribute__((always_inline)) {
     constexpr bool FAST = decltype(fast_tag)::value;
     // A step consumes C ring entries (1: a K tile of phase 0; 2: a tile's K
@@ -1878,6 +1887,8 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
               for (int h = 0; h < 2; ++h) lds_read_b64_tr16(base + (voff0[s][h] ^ (db << 5)), vr[db & 1][s][h]);
           };
           issue_v(std::integral_constant<int, 0>{});
+          f32x4 accv[DBLK];  // fast variant: the tile's weighted V, quantised after the range check
+          float vmax = 0.0f;
           static_for<DBLK>([&](auto dbc) {
             constexpr int db = decltype(dbc)::value;
             uint64_t(&cur)[NK0][2] = vr[db & 1];
@@ -1897,10 +1908,37 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
               acc = TR::mma(vb, pb[s], acc);
             }
             // lane: d = 16 db + 4 kg + e of its row
+            if constexpr (FAST) {
+              accv[db] = acc;
+              vmax = __builtin_elementwise_maximum(
+                  vmax, __builtin_elementwise_maximum(__builtin_elementwise_maximum(__builtin_fabsf(acc[0]), __builtin_fabsf(acc[1])),
+                                                      __builtin_elementwise_maximum(__builtin_fabsf(acc[2]), __builtin_fabsf(acc[3]))));
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wv[db][i] = wadd<BITS>(wv[db][i], quant<BITS>(__fmul_rn(acc[i], a.fxp_scale)));
+              for (int i = 0; i < 4; ++i) wv[db][i] = wadd<BITS>(wv[db][i], quant<BITS>(__fmul_rn(acc[i], a.fxp_scale)));
+            }
             __builtin_amdgcn_sched_barrier(0);
           });
+          if constexpr (FAST) {
+            // |acc| * 2^f below 2^22 (and the 16-bit range) for the whole
+            // wave: fl(acc * 2^f + 1.5 * 2^23) is RNE(acc * 2^f) + 1.5 * 2^23
+            // (exact product, one rounding, spacing 1, even constant), the
+            // bits quant gives; otherwise (large values, NaN) the exact path
+            if (__builtin_amdgcn_ballot_w64(!(vmax < vlim)) == 0) {
+#pragma unroll
+              for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                  wv[b][i] = static_cast<int32_t>(static_cast<uint32_t>(wv[b][i]) +
+                                                  __float_as_uint(__builtin_fmaf(accv[b][i], a.fxp_scale, 12582912.0f)) -
+                                                  0x4B400000u);
+            } else {
+#pragma unroll
+              for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wv[b][i] = wadd<BITS>(wv[b][i], quant<BITS>(__fmul_rn(accv[b][i], a.fxp_scale)));
+            }
+          }
         }
       }
       // the chunk's denominator over the row's four lanes, then the fold
