@@ -2093,11 +2093,16 @@ int launch_attn(const AttnArgs& a, int num_requests, int max_qtiles, int64_t num
         } else {
           attn_prefill_kernel<DT, BITS, DMAX><<<pgrid, kPThreads, 0, st>>>(b);
         }
+        // the short requests (fewer than kPrefillRows rows) span at most
+        // this many 16-row tiles: a grid over every tile of the longest
+        // request would only start workgroups that exit at once
+        const int64_t short_tiles = cdiv(kPrefillRows - 1, QROWS);
+        const dim3 sgrid(grid.x, unsigned(max_qtiles < short_tiles ? max_qtiles : short_tiles), 1);
         if (dma) {
-          const int e = launch_dma<DT, BITS, DMAX, false>(b, grid, st);
+          const int e = launch_dma<DT, BITS, DMAX, false>(b, sgrid, st);
           if (e) return e;
         } else {
-          attn_kernel<DT, BITS, DMAX, false><<<grid, kThreads, 0, st>>>(b);
+          attn_kernel<DT, BITS, DMAX, false><<<sgrid, kThreads, 0, st>>>(b);
         }
         return launch_status();
       }
