@@ -16,7 +16,7 @@ import torch
 import fxpr_vllm  # noqa: F401
 from fxpr_vllm._kernels import gemm as KG
 from oracle import gemm as G
-from tests._util import IO_NAME, close_report, from_np, mismatch_report, to_np
+from tests._util import IO_NAME, close_report, from_np, mismatch_report, nan_aware_equal, to_np
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -216,6 +216,33 @@ def test_gemm_big_split_k_invariance(dtype, M):
     for s in (1, 2, 3, 5, 8):  # 5: the last split has no K-tiles
         got = _run(a, b, bits=32, frac=16, split_k=s, b_layout="nk")
         assert torch.equal(got, want), (s, mismatch_report(got, want))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_int64_marked_tile_redo(dtype):
+    # unsplit 64-bit sums at M >= 1024 and f <= 20: 32-bit sums, tiles with a
+    # K-tile outside the rounding-constant range marked (NaN at the tile's
+    # first element) and recomputed by the 64-bit kernel. Here some K-tiles'
+    # quantised partials exceed 2^31 (a 32-bit sum would saturate) and a NaN
+    # bias column marks tiles that are in range (a redundant recompute); every
+    # row equals the same row of M = 512 launches (the 64-bit kernel
+    # throughout) bit for bit, NaN for NaN
+    g = torch.Generator("cpu").manual_seed(77)
+    M, K, N = 1024, 1024, 384
+    a = torch.randn(M, K, generator=g).to(dtype)
+    b = (torch.randn(K, N, generator=g) * 0.05).to(dtype)
+    # bf16: |P * 2^16| mostly beyond 2^31; f16 (max 65504): beyond the range check only
+    a[200:210, 128:256] = (a[200:210, 128:256].float() * (1e5 if dtype == torch.bfloat16 else 1e4)).to(dtype)
+    bias = torch.randn(N, generator=g).to(dtype)
+    bias[128] = float("nan")
+    full = _run(a, b, bias, bits=64, frac=16, b_layout="nk")
+    assert torch.isnan(full[:, 128]).all() and not torch.isnan(full[:, :128]).any()
+    for m0 in (0, 512):
+        part = _run(a[m0:m0 + 512].contiguous(), b, bias, bits=64, frac=16, b_layout="nk")
+        assert nan_aware_equal(part, full[m0:m0 + 512]), (m0, mismatch_report(part, full[m0:m0 + 512]))
+    want = _oracle(a[195:215], b, bias, 64, 16)
+    report = close_report(full[195:215], want)
+    assert not report, report
 
 
 # --- restated reference tests (fxpr_vllm/_tests/test_gemm.py) ---------------

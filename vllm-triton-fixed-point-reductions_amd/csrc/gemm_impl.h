@@ -85,6 +85,9 @@ struct GemmArgs {
   float fast_lim;
   int ktiles, tiles_per_split, tiles_m, tiles_n;
   int c_vec;         // C rows unit-stride, 16-byte aligned (vector row stores)
+  // gemm_big_kernel: compute only the output tiles whose first element C[m0][n0]
+  // is NaN (the marks of the int32-accumulating pass of a 64-bit launch)
+  int redo_marked;
 };
 
 template <int BITS> struct Acc { using T = int32_t; };
@@ -449,13 +452,20 @@ template <typename T> __device__ __forceinline__ void* uniform_ptr(const T* p) {
   return reinterpret_cast<void*>((uint64_t(hi) << 32) | lo);
 }
 
-template <int DT, int BITS, class BT, bool SPLIT>
+// WIDEN (BITS = 32, unsplit): the 64-bit accumulator semantics on 32-bit
+// sums. When every K-tile of an output tile quantises by the rounding
+// constant (|P * 2^f| < 2^22, so |q| < 2^22) and there are fewer than 512
+// K-tiles, the 32-bit sum cannot wrap and equals the 64-bit one; the epilogue
+// converts it as a 64-bit value. A tile with any K-tile outside that range
+// stores nothing but a NaN at C[m0][n0] for the 64-bit kernel's redo pass.
+template <int DT, int BITS, class BT, bool SPLIT, bool WIDEN = false>
 __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs args) {
   using M_ = Mma<DT>;
   using T = typename M_::T;
   using AccT = typename Acc<BITS>::T;
   static_assert(DT != FXPR_DTYPE_F32, "16-bit inputs only");
   static_assert(BT::MB == 4 && BT::NB == 4, "fragment asm assumes 64 x 64 wave tiles");
+  static_assert(!WIDEN || (BITS == 32 && !SPLIT), "WIDEN: unsplit 32-bit sums");
   constexpr int BM = BT::BM, BN = BT::BN, MB = BT::MB, NB = BT::NB, NW = BT::WAVES;
   constexpr int BKS = 64, CH = 8;
   constexpr int NSA = BT::NSA, NSB = BT::NSB;
@@ -477,6 +487,10 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, tm, tn);
   const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+  if (args.redo_marked) {  // uniform: one element per workgroup
+    const float c0 = Io<DT>::load(static_cast<const T*>(args.c)[m0 * args.scm + n0 * args.scn]);
+    if (!(c0 != c0)) return;
+  }
   const int split = blockIdx.y;
   const int kt_begin = split * args.tiles_per_split;
   const int kt_end = min(args.ktiles, kt_begin + args.tiles_per_split);
@@ -525,6 +539,7 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
 #pragma unroll
       for (int r = 0; r < 4; ++r) I[i][j][r] = 0;
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  bool out_of_range = false;  // WIDEN: a K-tile outside the rounding-constant range
 
   // Fragment reads: lane (row lane % 16 of each 16-row block, k slot kg)
   // reads chunk c = 4 h + kg of its row; the row's swizzle (row >> 1) & 7
@@ -778,6 +793,7 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     };
     for (int s = 0; s < nst; s += 2) {
       if (!tile_fast()) {  // rare: partials out of the fast range, NaN or infinite
+        if constexpr (WIDEN) out_of_range = true;
         quantize();
 #pragma unroll
         for (int i = 0; i < MB; ++i)
@@ -790,8 +806,29 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     lds_wait(fa0, fb0);                               // trailing reads (unused)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing DMAs into unused buffers
   }
+  if constexpr (WIDEN) {
+    if (!tile_fast()) out_of_range = true;  // the last K-tile
+  }
   quantize();
   __syncthreads();  // LDS is reused by the epilogue
+  if constexpr (WIDEN) {
+    // the workgroup's OR of the waves' range flags through the last words of
+    // the dynamic LDS (past the epilogue's area; __syncthreads_or would add
+    // static LDS, and 80 KB + a few bytes no longer fits two workgroups per
+    // CU); a marked tile stores only its mark
+    constexpr size_t FLAGS = big_lds_bytes<BT>() - 4 * NW;
+    static_assert(FLAGS >= size_t(NW) * BT::WM * (BT::WN + 8) * sizeof(T), "flags inside the epilogue's LDS");
+    int* flags = reinterpret_cast<int*>(smem_raw + FLAGS);
+    if (lane == 0) flags[wave] = out_of_range ? 1 : 0;
+    __syncthreads();
+    int any = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) any |= flags[w];
+    if (any) {
+      if (tid == 0) static_cast<T*>(args.c)[m0 * args.scm + n0 * args.scn] = Io<DT>::store(__builtin_nanf(""));
+      return;
+    }
+  }
 
   // Epilogue. Lane holds rows 4*(lane/16)+r of each 16x16 block, column lane%16.
   const int64_t row_base = m0 + wm * BT::WM + kg * 4;
@@ -820,7 +857,8 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       bv[j] = (bias && n < args.N) ? bias[n] : 0.0f;
     }
     auto value = [&](int i, int j, int r) {
-      float v = acc_to_f32<BITS>(I[i][j][r], args.inv_scale);
+      float v = WIDEN ? acc_to_f32<64>(static_cast<int64_t>(I[i][j][r]), args.inv_scale)
+                      : acc_to_f32<BITS>(I[i][j][r], args.inv_scale);
       if (bias) v = __fadd_rn(v, bv[j]);
       return Io<DT>::store(v);
     };
@@ -893,7 +931,7 @@ int launch_tile(const GemmArgs& a, int splits, hipStream_t st) {
   return launch_status();
 }
 
-template <int DT, int BITS, class BT>
+template <int DT, int BITS, class BT, bool WIDEN = false>
 int launch_big(GemmArgs a, int splits, hipStream_t st) {
   a.tiles_m = int(cdiv(a.M, BT::BM));
   a.tiles_n = int(cdiv(a.N, BT::BN));
@@ -909,8 +947,12 @@ int launch_big(GemmArgs a, int splits, hipStream_t st) {
     kern<<<dim3(unsigned(a.tiles_m * a.tiles_n), unsigned(splits)), BT::THREADS, lds, st>>>(a);
     return launch_status();
   };
-  if (splits > 1) return go(gemm_big_kernel<DT, BITS, BT, true>);
-  return go(gemm_big_kernel<DT, BITS, BT, false>);
+  if constexpr (WIDEN) {
+    return go(gemm_big_kernel<DT, BITS, BT, false, true>);
+  } else {
+    if (splits > 1) return go(gemm_big_kernel<DT, BITS, BT, true>);
+    return go(gemm_big_kernel<DT, BITS, BT, false>);
+  }
 }
 
 template <int DT, int BITS, class TL, bool BNC, bool VEC>
@@ -955,7 +997,22 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
   const bool big_ok = vec && !b_ncontig && t == TileId::Big && a.lda <= (int64_t(1) << 22) &&
                       a.ldb <= (int64_t(1) << 22);
   if constexpr (DT != FXPR_DTYPE_F32 && BITS == 64) {
-    if (big_ok) return launch_big<DT, BITS, TB64>(a, splits, st);
+    if (big_ok) {
+      // Unsplit, M >= 1024, fewer than 512 K-tiles: 32-bit sums in the
+      // two-workgroups-per-CU schedule (the 64-bit state of the exact kernel
+      // leaves it one wave per SIMD), then the exact kernel on the tiles that
+      // pass marked (a K-tile outside the rounding-constant range). Only for
+      // f <= 20 (|P| < 4 per K-tile stays in range; at larger f most tiles
+      // would be computed twice).
+      if (splits <= 1 && a.M >= 1024 && a.ktiles < 512 && a.fast_lim >= 4.0f) {
+        const int rc = launch_big<DT, 32, TB2, true>(a, 1, st);
+        if (rc != FXPR_OK) return rc;
+        GemmArgs b = a;
+        b.redo_marked = 1;
+        return launch_big<DT, BITS, TB64>(b, 1, st);
+      }
+      return launch_big<DT, BITS, TB64>(a, splits, st);
+    }
   }
   if constexpr (DT != FXPR_DTYPE_F32 && BITS != 64) {
     if (big_ok) {
