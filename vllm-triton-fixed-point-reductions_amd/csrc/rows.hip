@@ -36,15 +36,27 @@ __device__ __forceinline__ __int128 shfl_xor_i128(__int128 v, int o) {
   return static_cast<__int128>((static_cast<unsigned __int128>(hi) << 64) | lo);
 }
 
-template <int QBITS, int OBITS>
+// VEC > 1: rows of 16-byte vectors (cols a multiple of VEC, q 16-byte aligned).
+template <int QBITS, int OBITS, int VEC>
 __global__ __launch_bounds__(256) void row_sum_kernel(
     const typename RowSumTypes<QBITS>::Q* __restrict__ q, void* __restrict__ out, int64_t cols) {
+  using Q = typename RowSumTypes<QBITS>::Q;
   using Acc = typename RowSumTypes<QBITS>::Acc;
   __shared__ Acc smem[4];
   const int64_t row = blockIdx.x;
   const auto* p = q + row * cols;
   Acc acc = 0;
-  for (int64_t j = threadIdx.x; j < cols; j += 256) acc += static_cast<Acc>(p[j]);
+  if constexpr (VEC > 1) {
+    using V = Vec<Q, VEC>;
+    const V* pv = reinterpret_cast<const V*>(p);
+    for (int64_t j = threadIdx.x; j < cols / VEC; j += 256) {
+      const V v = pv[j];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc += static_cast<Acc>(v.v[e]);
+    }
+  } else {
+    for (int64_t j = threadIdx.x; j < cols; j += 256) acc += static_cast<Acc>(p[j]);
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     if constexpr (QBITS == 64) acc += shfl_xor_i128(acc, o);
@@ -63,17 +75,25 @@ __global__ __launch_bounds__(256) void row_sum_kernel(
   }
 }
 
-template <int QBITS>
-int launch_row_sum(const void* q, void* out, int obits, int64_t rows, int64_t cols, hipStream_t st) {
+template <int QBITS, int VEC>
+int launch_row_sum_vec(const void* q, void* out, int obits, int64_t rows, int64_t cols, hipStream_t st) {
   using Q = typename RowSumTypes<QBITS>::Q;
   const Q* qp = static_cast<const Q*>(q);
   dim3 grid(static_cast<unsigned>(rows));
   switch (obits) {
-    case 16: row_sum_kernel<QBITS, 16><<<grid, 256, 0, st>>>(qp, out, cols); break;
-    case 32: row_sum_kernel<QBITS, 32><<<grid, 256, 0, st>>>(qp, out, cols); break;
-    default: row_sum_kernel<QBITS, 64><<<grid, 256, 0, st>>>(qp, out, cols); break;
+    case 16: row_sum_kernel<QBITS, 16, VEC><<<grid, 256, 0, st>>>(qp, out, cols); break;
+    case 32: row_sum_kernel<QBITS, 32, VEC><<<grid, 256, 0, st>>>(qp, out, cols); break;
+    default: row_sum_kernel<QBITS, 64, VEC><<<grid, 256, 0, st>>>(qp, out, cols); break;
   }
   return launch_status();
+}
+
+// 16-byte loads when every row starts 16-byte aligned.
+template <int QBITS>
+int launch_row_sum(const void* q, void* out, int obits, int64_t rows, int64_t cols, hipStream_t st) {
+  constexpr int VEC = 128 / QBITS;
+  if (cols % VEC == 0 && aligned(q, 16)) return launch_row_sum_vec<QBITS, VEC>(q, out, obits, rows, cols, st);
+  return launch_row_sum_vec<QBITS, 1>(q, out, obits, rows, cols, st);
 }
 
 // ---------------------------------------------------------------------------
