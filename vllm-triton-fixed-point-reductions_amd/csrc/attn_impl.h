@@ -1751,10 +1751,12 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     auto stage_base = [&](int e) -> unsigned { return lds0 + (e % NS) * G::TILEB; };
     // The four transposed score MFMA chains of the tile at base (q = 2 s + h),
     // software-pipelined: chain q + 1's fragment reads are issued before chain
-    // q's wait, MFMAs and fn(q, acc) (only the newest chain's QSTEPS reads may
-    // remain in flight at the wait).
+    // q's wait and MFMAs (only the newest chain's QSTEPS reads may remain in
+    // flight at the wait). At head_dim 128, fn(q - 1, acc) runs while chain
+    // q's MFMAs do (at 64 the extra live registers cost a workgroup per CU).
     auto key_groups = [&](unsigned base, auto&& fn) __attribute__((always_inline)) {
       u32x4 kf[2][QSTEPS];
+      f32x4 accs[2];
       auto issue = [&](auto qc) __attribute__((always_inline)) {
         constexpr int q = decltype(qc)::value;
         static_for<QSTEPS>([&](auto jc) {
@@ -1777,9 +1779,15 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < QSTEPS; ++j) acc = TR::mma(cur[j], qf[j], acc);
-        fn(qc, acc);
+        if constexpr (QSTEPS == 4) {
+          accs[q & 1] = acc;
+          if constexpr (q > 0) fn(std::integral_constant<int, q - 1>{}, accs[(q - 1) & 1]);
+        } else {
+          fn(qc, acc);
+        }
         __builtin_amdgcn_sched_barrier(0);
       });
+      if constexpr (QSTEPS == 4) fn(std::integral_constant<int, 3>{}, accs[1]);
     };
     // Scores of chain q of tile t for the lane's row and keys
     // t * TILE + 32 (q >> 1) + 8 kg + 4 (q & 1) + e; whole: the wave's rows see
@@ -1947,11 +1955,28 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       if (mx != -__builtin_inff()) {  // else no key of the row in this chunk
         float Mn, fa, fb;
         merge_factors(Mr, mx, Mn, fa, fb);
-        Dr = wadd<BITS>(rescale<BITS>(Dr, fa), rescale<BITS>(den, fb));
+        // Mn is M or mc, so fa or fb is 2^0 = 1 unless both maxima are +inf
+        // (then inf - inf: NaN). rescale(x, 1) = x for 16- and 32-bit sums
+        // (exact in fp64; 16-bit sums are read modulo 2^16 everywhere), so
+        // the fold rescales one side only. 64-bit sums round through fp64.
+        const bool one_a = fa == 1.0f;
+        if (BITS != 64 && __builtin_amdgcn_ballot_w64(!(one_a || fb == 1.0f)) == 0) {
+          const float f = one_a ? fb : fa;
+          Dr = wadd<BITS>(rescale<BITS>(one_a ? den : Dr, f), one_a ? Dr : den);
 #pragma unroll
-        for (int b = 0; b < DBLK; ++b)
+          for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) Wr[b][i] = wadd<BITS>(rescale<BITS>(Wr[b][i], fa), rescale<BITS>(wv[b][i], fb));
+            for (int i = 0; i < 4; ++i) {
+              const AccT x = one_a ? wv[b][i] : Wr[b][i], y = one_a ? Wr[b][i] : wv[b][i];
+              Wr[b][i] = wadd<BITS>(rescale<BITS>(x, f), y);
+            }
+        } else {
+          Dr = wadd<BITS>(rescale<BITS>(Dr, fa), rescale<BITS>(den, fb));
+#pragma unroll
+          for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Wr[b][i] = wadd<BITS>(rescale<BITS>(Wr[b][i], fa), rescale<BITS>(wv[b][i], fb));
+        }
         Mr = Mn;
       }
     }
