@@ -334,6 +334,47 @@ def test_config4_decode_full_shape_properties():
     assert int(sl[longest]) > 7680  # 16 chunks of 512 keys
 
 
+@pytest.mark.parametrize("R", [63, 200, 256, 257])
+def test_decode_request_order_many_requests_with_ties(R):
+    # Unsplit and multi-chunk split launches dispatch the requests longest
+    # first (ties by index; up to 256 requests), the one-chunk splits of the
+    # automatic plan in launch order. The order must be a permutation: every
+    # row written once (outputs start as NaN) and the bits of every split
+    # count equal; rows of a short, a tied and the longest request against
+    # the oracle.
+    g = torch.Generator("cpu").manual_seed(R)
+    hq, hkv, d, ps = 8, 2, 128, 16
+    choices = torch.tensor([1, 17, 511, 512, 513, 1500, 2600], dtype=torch.int32)
+    sl = choices[torch.randint(0, len(choices), (R,), generator=g)]
+    maxb = (int(sl.max()) + ps - 1) // ps
+    pool = R * maxb
+    bt = torch.randperm(pool, generator=g).to(torch.int32).reshape(R, maxb)
+    q = torch.randn(R, hq, d, generator=g).to(torch.bfloat16).to(DEV)
+    gd = torch.Generator(DEV).manual_seed(2)
+    kv = torch.randn(pool, 2, ps, hkv, d, generator=gd, device=DEV, dtype=torch.bfloat16)
+    qsl = torch.arange(R + 1, dtype=torch.int32, device=DEV)
+    sl_d, bt_d = sl.to(DEV), bt.to(DEV)
+
+    def run(splits):
+        o = torch.full_like(q, float("nan"))
+        torch.ops.fxpr.unified_attention_fxp(q, kv, o, qsl, sl_d, bt_d, 1, None, True, None, 32, 16, 0.0, 0,
+                                             splits)
+        assert not torch.isnan(o).any(), splits
+        return o
+
+    ref = run(0)
+    for s in (1, 2, 3):
+        assert torch.equal(run(s), ref), s
+    longest = int(torch.argmax(sl))
+    tied = [i for i in range(R) if int(sl[i]) == int(sl[longest]) and i != longest]
+    for r in [int(torch.argmin(sl)), longest] + tied[:1]:
+        nblk = (int(sl[r]) + ps - 1) // ps
+        sub_kv = kv[bt[r, :nblk].long().to(DEV)].cpu()
+        sub_bt = torch.arange(nblk, dtype=torch.int32).reshape(1, nblk)
+        sub = (q[r:r + 1].cpu(), sub_kv, torch.tensor([0, 1], dtype=torch.int32), sl[r:r + 1], sub_bt)
+        assert close(ref[r:r + 1], oracle(*sub))
+
+
 # --------------------------------------------------------------------------
 # 128-row prefill workgroups (16-bit inputs, Q <= 32-bit accumulators,
 # head_dim <= 128, one split, max_query_len * group >= 113) against the

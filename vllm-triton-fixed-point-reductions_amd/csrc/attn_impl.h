@@ -677,32 +677,57 @@ constexpr int kCpolNT = 2;
 // for up to kOrderMax of them: request_by_length(a, k) is the k-th longest,
 // so the workgroups of the requests that bound the launch are dispatched
 // first, and (with two workgroups per CU placed in dispatch order) a long
-// request's workgroup tends to share its CU with a short one's. Wave-uniform;
-// each wave ranks 64 requests per pass with scalar loads of the lengths
-// (about half a microsecond: launches whose workgroups hold at most one
-// chunk each keep the launch order, the ranking would cost more than the
-// order gains).
+// request's workgroup tends to share its CU with a short one's. Only the
+// dispatch order depends on it, never a bit of the results; it must be a
+// permutation of the requests. Wave-uniform, all lanes active: the lane
+// holds the lengths of requests lane + 64 j (negative lengths count as 0),
+// a radix select over the length bits finds the (k + 1)-th largest length T
+// (31 steps of kOrderMax / 64 ballots), then the requests of length T are
+// taken in index order. Launches whose workgroups hold at most one chunk
+// each keep the launch order (the order gains nothing there).
 constexpr int kOrderMax = 256;
 __device__ __forceinline__ int request_by_length(const AttnArgs& a, int k) {
   const int R = a.num_requests;
   const int per_max = a.num_splits <= 1 ? a.chunk_slots + 1
                       : a.chunks_per_split > 0 ? a.chunks_per_split
                                                : (a.chunk_slots + a.num_splits - 1) / a.num_splits;
-  if (R <= 1 || R > kOrderMax || per_max <= 1) return k;
-  const ConstI32Ptr sls = (ConstI32Ptr)a.seq_lens;
+  if (R <= 1 || R > kOrderMax || k >= R || per_max <= 1) return k;
+  constexpr int NB = kOrderMax / 64;
   const int lane = threadIdx.x & 63;
-  for (int i0 = 0; i0 < R; i0 += 64) {
-    const int i = i0 + lane;
-    const int li = i < R ? a.seq_lens[i] : 0;
-    int rank = 0;
-    for (int kk = 0; kk < R; ++kk) {
-      const int lk = sls[kk];
-      rank += (lk > li || (lk == li && kk < i)) ? 1 : 0;
-    }
-    const uint64_t m = __builtin_amdgcn_ballot_w64(i < R && rank == k);
-    if (m) return i0 + __builtin_ctzll(m);
+  int len[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int i = 64 * j + lane;
+    len[j] = i < R ? max(a.seq_lens[i], 0) : -1;  // -1: no request, below every candidate
   }
-  return k;  // not reached: ranks are a permutation of 0 .. R - 1
+  auto count_ge = [&](int v) {
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(len[j] >= v));
+    return c;
+  };
+  // the largest T >= 0 with more than k lengths >= T
+  int T = 0;
+  for (int b = 30; b >= 0; --b) {
+    const int cand = T | (1 << b);
+    if (count_ge(cand) > k) T = cand;
+  }
+  int greater = 0;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) greater += __builtin_popcountll(__builtin_amdgcn_ballot_w64(len[j] > T));
+  int rr = k - greater;  // rank among the requests of length T, by index
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64(len[j] == T);
+    const int n = __builtin_popcountll(m);
+    if (rr < n) {
+      const int below = int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(len[j] == T && below == rr);
+      return 64 * j + __builtin_ctzll(hit);
+    }
+    rr -= n;
+  }
+  return k;  // not reached: greater <= k < greater + (count of T)
 }
 
 // Wait for the DMAs of a step when `later` steps' DMAs (NDMA instructions
@@ -2017,33 +2042,46 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t n
   if (idx >= total) return;
   const int d = int(idx % a.head_dim);
   const int64_t th = idx / a.head_dim;  // token * Hq + head
-  const int c0 = max(0, a.crange[2 * th]), c1 = min(a.chunk_slots, a.crange[2 * th + 1]);
   float M = -__builtin_inff();
   AccT D = 0, W = 0;
   // batches of NB chunks: every load of a batch is issued (clamped to the
   // range) before the sequential fold, so the loads overlap
-  constexpr int NB = 8;
+  constexpr int NB = 16;
   const AccT* den_p = static_cast<const AccT*>(a.den_ws) + th * a.chunk_slots;
   const AccT* wv_p = static_cast<const AccT*>(a.wv_ws) + th * a.chunk_slots * a.head_dim + d;
   const float* pm_p = a.pmax + th * a.chunk_slots;
-  for (int cb = c0; cb < c1; cb += NB) {
-    float mc[NB];
-    AccT dc[NB], wc[NB];
+  float mc[NB];
+  AccT dc[NB], wc[NB];
+  auto load = [&](int cb, int c_end) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
-      const int c = min(cb + k, c1 - 1);
+      const int c = min(cb + k, c_end - 1);
       mc[k] = pm_p[c];
       dc[k] = den_p[c];
       wc[k] = wv_p[int64_t(c) * a.head_dim];
     }
+  };
+  auto fold = [&](int cb, int c_end) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
-      if (cb + k >= c1 || mc[k] == -__builtin_inff()) continue;
+      if (cb + k >= c_end || mc[k] == -__builtin_inff()) continue;
       float Mn, fa, fb;
       merge_factors(M, mc[k], Mn, fa, fb);
       D = wadd<BITS>(rescale<BITS>(D, fa), rescale<BITS>(dc[k], fb));
       W = wadd<BITS>(rescale<BITS>(W, fa), rescale<BITS>(wc[k], fb));
       M = Mn;
+    }
+  };
+  // The first batch goes out with the range loads (the range of a row
+  // usually starts at chunk 0 and fits one batch): one round trip, not two.
+  if (a.chunk_slots > 0) load(0, a.chunk_slots);
+  const int c0 = max(0, a.crange[2 * th]), c1 = min(a.chunk_slots, a.crange[2 * th + 1]);
+  if (c0 == 0 && c1 <= NB) {
+    fold(0, c1);
+  } else {
+    for (int cb = c0; cb < c1; cb += NB) {
+      load(cb, c1);
+      fold(cb, c1);
     }
   }
   const float den_f = fmaxf(acc_f32<BITS>(D, a.fxp_inv), 1.0e-6f);
