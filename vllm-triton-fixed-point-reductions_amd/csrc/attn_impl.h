@@ -1666,14 +1666,24 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       didx = 2 * nt - 1;
     }
   };
-  int dent = 0;
+  // The page entry of the cursor's tile, loaded when the cursor moves to
+  // another tile: a tile's V entry follows its K entry in phase 1 and reuses
+  // it (a reload there would be waited for by the very next DMA).
+  int dent = 0, dent_t = -1;
+  auto refresh_entry = [&]() {
+    const int t = cur_tile();
+    if (t != dent_t) {
+      dent = page_entry(t);
+      dent_t = t;
+    }
+  };
   if (c_lo < c_hi) {
-    dent = page_entry(cur_tile());
+    refresh_entry();
 #pragma unroll
     for (int i = 0; i + 2 < NS; ++i) {
       dma_tile(cur_isv(), cur_tile(), dent, i);
       advance();
-      dent = page_entry(cur_tile());
+      refresh_entry();
     }
   }
 
@@ -1767,7 +1777,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       for (int u = 0; u < C; ++u) {
         dma_tile(cur_isv(), cur_tile(), dent, (step + NS - 2 + u) % NS);
         advance();
-        dent = page_entry(cur_tile());
+        refresh_entry();
       }
       const int e = step;
       step += C;
