@@ -133,7 +133,7 @@ def test_gemm_deterministic_across_runs():
 # otherwise. Inputs below keep every K-tile dot exact in fp32, so the result
 # must equal the oracle bit for bit on either path.
 
-_BIG_M = [256, 1024]  # 8-wave 256 x 128 tiles below M = 1024, 4-wave 128 x 128 from there
+_BIG_M = [256, 1024]  # 128 x 128 tiles; 64-bit sums: the 32-bit schedule plus redo from M = 1024
 
 
 def _dyadic(shape, lo, hi, exp2, g, dtype):
@@ -220,12 +220,12 @@ def test_gemm_big_split_k_invariance(dtype, M):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_int64_marked_tile_redo(dtype):
-    # unsplit 64-bit sums at M >= 1024 and f <= 20: 32-bit sums, tiles with a
+    # unsplit 64-bit sums at M > 64 and f <= 20: 32-bit sums, tiles with a
     # K-tile outside the rounding-constant range marked (NaN at the tile's
     # first element) and recomputed by the 64-bit kernel. Here some K-tiles'
     # quantised partials exceed 2^31 (a 32-bit sum would saturate) and a NaN
     # bias column marks tiles that are in range (a redundant recompute); every
-    # row equals the same row of M = 512 launches (the 64-bit kernel
+    # row equals the same row of split M = 512 launches (the 64-bit kernel
     # throughout) bit for bit, NaN for NaN
     g = torch.Generator("cpu").manual_seed(77)
     M, K, N = 1024, 1024, 384
@@ -238,7 +238,7 @@ def test_gemm_int64_marked_tile_redo(dtype):
     full = _run(a, b, bias, bits=64, frac=16, b_layout="nk")
     assert torch.isnan(full[:, 128]).all() and not torch.isnan(full[:, :128]).any()
     for m0 in (0, 512):
-        part = _run(a[m0:m0 + 512].contiguous(), b, bias, bits=64, frac=16, b_layout="nk")
+        part = _run(a[m0:m0 + 512].contiguous(), b, bias, bits=64, frac=16, b_layout="nk", split_k=2)
         assert nan_aware_equal(part, full[m0:m0 + 512]), (m0, mismatch_report(part, full[m0:m0 + 512]))
     want = _oracle(a[195:215], b, bias, 64, 16)
     report = close_report(full[195:215], want)
@@ -334,12 +334,13 @@ def test_lm_head_full_vocab_properties():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M", [1024, 2048])
-@pytest.mark.parametrize("bits,frac", [(32, 16), (64, 16)])
+@pytest.mark.parametrize("bits,frac", [(32, 16), (64, 16), (64, 24)])
 def test_gemm_k4096_steady_state_exact(dtype, M, bits, frac):
     # dyadic inputs whose tile dots are exact in fp32 (|P| up to 2^13 * 2^-7
     # against the fast range 2^6 at Q16: a mix of rounding-constant and exact
     # K-tiles), bit for bit against the oracle; the two-workgroup 128 x 128
-    # config (M >= 1024) and the int64 config over the whole K
+    # config, 64-bit sums by the 32-bit schedule plus redo (Q16) and by the
+    # one-wave-per-SIMD exact kernel over the whole K (Q24: f > 20)
     g = torch.Generator("cpu").manual_seed(M + bits)
     K, N = 4096, 640
     a = _dyadic((M, K), -4, 4, -7, g, dtype)
@@ -366,7 +367,7 @@ def _lm_head_inputs(M, N, K, seed, dtype=torch.bfloat16, b_std=0.02):
 def test_lm_head_headline_m8192(bits):
     # BASELINE config 3 at the bench's M = 8192 (K = 4096, N = 128256): the
     # rows of the M = 8192 launch equal the same rows computed at M = 1, 32,
-    # 256 and 2048 (skinny tiles, 8-wave and 4-wave large-M tiles), a split
+    # 256 and 2048 (skinny and large-M tiles), a split
     # launch gives the same bits, and a row x column block is within 1e-2 of
     # the oracle
     K, N, M = 4096, 128256, 8192

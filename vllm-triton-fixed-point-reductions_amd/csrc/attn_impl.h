@@ -696,10 +696,13 @@ __device__ __forceinline__ int request_by_length(const AttnArgs& a, int k) {
   const int lane = threadIdx.x & 63;
   int len[NB];
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int i = 64 * j + lane;
-    len[j] = i < R ? max(a.seq_lens[i], 0) : -1;  // -1: no request, below every candidate
-  }
+  for (int j = 0; j < NB; ++j) len[j] = a.seq_lens[min(64 * j + lane, R - 1)];
+  // (through the asm the loads are unconditional, issued together and waited
+  // for once; the compiler would otherwise predicate each behind a wait)
+  static_assert(NB == 4, "four length blocks");
+  asm volatile("" : "+v"(len[0]), "+v"(len[1]), "+v"(len[2]), "+v"(len[3]));
+#pragma unroll
+  for (int j = 0; j < NB; ++j) len[j] = 64 * j + lane < R ? max(len[j], 0) : -1;  // -1: no request
   auto count_ge = [&](int v) {
     int c = 0;
 #pragma unroll

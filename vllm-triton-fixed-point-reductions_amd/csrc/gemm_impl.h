@@ -381,10 +381,9 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, 
 // increasing k, zero C at each 128-wide K-tile), so results are bitwise
 // identical to every other configuration; only the schedule differs.
 //
-// Waves of 64 x 64 outputs, two per SIMD: one 8-wave workgroup per CU over a
-// 256 x 128 tile with three LDS stages, or two 4-wave workgroups per CU over
-// 128 x 128 tiles with two stages each (the two waves of a SIMD then belong
-// to different workgroups and never wait on the same barrier).
+// Waves of 64 x 64 outputs, two per SIMD: two 4-wave workgroups per CU over
+// 128 x 128 tiles (the two waves of a SIMD belong to different workgroups and
+// never wait on the same barrier); with 64-bit sums one wave per SIMD.
 // A and B stages (64 k) go straight from global memory into LDS with
 // global_load_lds_dwordx4 (no staging registers).
 // Rows are 128 B with the 16-byte chunk c of row r stored at slot
@@ -408,8 +407,9 @@ template <int BM_, int BN_, int WGM_, int WGN_, int NSA_, int NSB_, int WPE_ = 2
   static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int MB = WM / 16, NB = WN / 16;
 };
-using TB = BigTile<256, 128, 4, 2, 3, 3>;   // one 8-wave workgroup per CU
-// two 4-wave workgroups per CU (80 KB of LDS each)
+// two 4-wave workgroups per CU (80 KB of LDS each), every M > 64: one 8-wave
+// 256 x 128 workgroup per CU measured the same at M = 256 .. 1024 and 1.6-1.8x
+// slower at M = 65 .. 128 (half its rows past M)
 #ifndef FXPR_TB2_NSB
 #define FXPR_TB2_NSB 3
 #endif
@@ -998,13 +998,13 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
                       a.ldb <= (int64_t(1) << 22);
   if constexpr (DT != FXPR_DTYPE_F32 && BITS == 64) {
     if (big_ok) {
-      // Unsplit, M >= 1024, fewer than 512 K-tiles: 32-bit sums in the
-      // two-workgroups-per-CU schedule (the 64-bit state of the exact kernel
-      // leaves it one wave per SIMD), then the exact kernel on the tiles that
-      // pass marked (a K-tile outside the rounding-constant range). Only for
-      // f <= 20 (|P| < 4 per K-tile stays in range; at larger f most tiles
-      // would be computed twice).
-      if (splits <= 1 && a.M >= 1024 && a.ktiles < 512 && a.fast_lim >= 4.0f) {
+      // Unsplit, fewer than 512 K-tiles: 32-bit sums in the two-workgroups-
+      // per-CU schedule (the 64-bit state of the exact kernel leaves it one
+      // wave per SIMD), then the exact kernel on the tiles that pass marked (a
+      // K-tile outside the rounding-constant range). Only for f <= 20 (|P| < 4
+      // per K-tile stays in range; at larger f most tiles would be computed
+      // twice). 1.4-1.8x faster than the exact kernel alone from M = 65 up.
+      if (splits <= 1 && a.ktiles < 512 && a.fast_lim >= 4.0f) {
         const int rc = launch_big<DT, 32, TB2, true>(a, 1, st);
         if (rc != FXPR_OK) return rc;
         GemmArgs b = a;
@@ -1015,12 +1015,7 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
     }
   }
   if constexpr (DT != FXPR_DTYPE_F32 && BITS != 64) {
-    if (big_ok) {
-      // two 4-wave workgroups per CU from M = 1024 (6 % faster at M = 8192),
-      // one 8-wave workgroup below (fewer, larger tiles while HBM-bound)
-      if (a.M >= 1024) return launch_big<DT, BITS, TB2>(a, splits, st);
-      return launch_big<DT, BITS, TB>(a, splits, st);
-    }
+    if (big_ok) return launch_big<DT, BITS, TB2>(a, splits, st);
   }
   if (vec && !b_ncontig) {
     switch (t) {
@@ -1061,8 +1056,8 @@ inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int req
     int bm, bn;
     tile_dims(pick_tile(M), bm, bn);
     if (pick_tile(M) == TileId::Big && io_dtype != FXPR_DTYPE_F32) {
-      bm = M >= 1024 ? TB2::BM : TB::BM;
-      bn = M >= 1024 ? TB2::BN : TB::BN;
+      bm = TB2::BM;  // TB64 has the same tile
+      bn = TB2::BN;
     }
     const int64_t tiles = cdiv(M, bm) * cdiv(N, bn);
     if (tiles >= 256) return 1;
