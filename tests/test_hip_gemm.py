@@ -127,7 +127,7 @@ def test_gemm_deterministic_across_runs():
 
 
 # --- large-M kernel: rounding-constant quantisation and its exact fallback ---
-# gemm_big_kernel (16-bit inputs, M > 64, K-contiguous B) quantises a wave's
+# gemm_big_kernel (16-bit inputs, M > 16, K-contiguous B) quantises a wave's
 # K-tile by the rounding constant 1.5 * 2^23 when every partial satisfies
 # |P| < 2^22 / 2^f (32767 / 2^f for 16-bit accumulators), and exactly
 # otherwise. Inputs below keep every K-tile dot exact in fp32, so the result
@@ -220,7 +220,7 @@ def test_gemm_big_split_k_invariance(dtype, M):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_int64_marked_tile_redo(dtype):
-    # unsplit 64-bit sums at M > 64 and f <= 20: 32-bit sums, tiles with a
+    # unsplit 64-bit sums at M > 16 and f <= 20: 32-bit sums, tiles with a
     # K-tile outside the rounding-constant range marked (NaN at the tile's
     # first element) and recomputed by the 64-bit kernel. Here some K-tiles'
     # quantised partials exceed 2^31 (a 32-bit sum would saturate) and a NaN
@@ -310,8 +310,9 @@ def test_gemm_errors_and_empty():
 
 def test_lm_head_full_vocab_properties():
     # config-3 shape at M=1 and M=32: full N=128256, K=4096. Batch invariance
-    # across the skinny tile configs, split invariance, and an oracle check on
-    # a column sample (the oracle at full size would take minutes).
+    # across the skinny (M = 1, 16) and large-M (M = 32) tiles, split
+    # invariance, and an oracle check on a column sample (the oracle at full
+    # size would take minutes).
     g = torch.Generator("cpu").manual_seed(0)
     K, N = 4096, 128256
     a = torch.randn(32, K, generator=g).to(torch.bfloat16)
@@ -320,6 +321,8 @@ def test_lm_head_full_vocab_properties():
     c32 = KG.gemm_fxp_run(a.to(DEV), bd, None, 32, 16)
     c1 = KG.gemm_fxp_run(a[:1].to(DEV), bd, None, 32, 16)
     assert torch.equal(c1[0], c32[0])
+    c16 = KG.gemm_fxp_run(a[:16].to(DEV), bd, None, 32, 16)
+    assert torch.equal(c16, c32[:16])
     c32s = KG.gemm_fxp_run(a.to(DEV), bd, None, 32, 16, split_k=4)
     assert torch.equal(c32s, c32)
     cols = torch.randperm(N, generator=g)[:512]

@@ -407,7 +407,7 @@ template <int BM_, int BN_, int WGM_, int WGN_, int NSA_, int NSB_, int WPE_ = 2
   static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int MB = WM / 16, NB = WN / 16;
 };
-// two 4-wave workgroups per CU (80 KB of LDS each), every M > 64: one 8-wave
+// two 4-wave workgroups per CU (80 KB of LDS each), every M > 16: one 8-wave
 // 256 x 128 workgroup per CU measured the same at M = 256 .. 1024 and 1.6-1.8x
 // slower at M = 65 .. 128 (half its rows past M)
 #ifndef FXPR_TB2_NSB
@@ -977,6 +977,9 @@ using T32 = Tile<32, 256, 32, 64>;
 using T64 = Tile<64, 256, 64, 64>;
 using TBig = Tile<128, 128, 64, 64>;
 
+// rows for which 16-bit K-contiguous operands take gemm_big_kernel
+inline bool big_rows(int64_t M) { return M > 16; }
+
 inline void tile_dims(TileId t, int& bm, int& bn) {
   switch (t) {
     case TileId::M16: bm = T16::BM; bn = T16::BN; break;
@@ -993,8 +996,12 @@ inline void tile_dims(TileId t, int& bm, int& bn) {
 template <int DT, int BITS>
 int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
   const TileId t = pick_tile(a.M);
-  // gemm_big_kernel's 32-bit lane offsets span up to 256 rows of A or B
-  const bool big_ok = vec && !b_ncontig && t == TileId::Big && a.lda <= (int64_t(1) << 22) &&
+  // gemm_big_kernel's 32-bit lane offsets span up to 256 rows of A or B.
+  // From M = 17 its 128 x 128 tiles (rows past M clamped, never stored) beat
+  // the skinny tiles: 183 / 187 us against 215 / 244 at M = 32 / 64 (64-bit
+  // sums: 189 / 192 against 245 / 362); at M <= 16 the skinny tile streams B
+  // faster (153 against 176 us).
+  const bool big_ok = vec && !b_ncontig && big_rows(a.M) && a.lda <= (int64_t(1) << 22) &&
                       a.ldb <= (int64_t(1) << 22);
   if constexpr (DT != FXPR_DTYPE_F32 && BITS == 64) {
     if (big_ok) {
@@ -1055,7 +1062,7 @@ inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int req
   } else {
     int bm, bn;
     tile_dims(pick_tile(M), bm, bn);
-    if (pick_tile(M) == TileId::Big && io_dtype != FXPR_DTYPE_F32) {
+    if (big_rows(M) && io_dtype != FXPR_DTYPE_F32) {
       bm = TB2::BM;  // TB64 has the same tile
       bn = TB2::BN;
     }
