@@ -1610,16 +1610,19 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   // branch on isv (a select between the two matrices' fields becomes a load
   // through a selected address, which keeps the captured values in scratch
   // memory, reloaded at every DMA; those reloads' vmcnt waits drain the ring).
-  // Per-lane parts of the DMA sources, fixed for the kernel: the row of the
-  // wave's instruction q and its chunk offset under the K and V swizzles.
-  int dma_rr[G::NDMA];
-  uint32_t dma_ck[G::NDMA], dma_cv[G::NDMA];
+  // Per-lane byte offsets of the DMA sources, fixed for the kernel: row
+  // q KPI + lane / CPR of the wave's 16 key rows of a tile, chunk slot
+  // (lane % CPR) ^ the K or V swizzle of its tile row. The wave's 16 rows lie
+  // in one page (pages hold 16 keys or more, the rows start 16-aligned), so
+  // a whole tile's sources are a uniform base (page, head, the wave's first
+  // row) plus these offsets; the last, partial tile of a request clamps its
+  // keys per lane instead. (The host keeps 16 key strides below 2^26 bytes.)
+  uint32_t dma_ok[G::NDMA], dma_ov[G::NDMA];
 #pragma unroll
   for (int q = 0; q < G::NDMA; ++q) {
-    const int rr = G::RPW * wave + q * G::KPI + lane / G::CPR;
-    dma_rr[q] = rr;
-    dma_ck[q] = uint32_t(((lane % G::CPR) ^ G::kswz(rr)) * 8);
-    dma_cv[q] = uint32_t(((lane % G::CPR) ^ SW::swz(rr)) * 8);
+    const int lr = q * G::KPI + lane / G::CPR, rr = G::RPW * wave + lr;
+    dma_ok[q] = (uint32_t(lr) * uint32_t(a.sk_s) + uint32_t(((lane % G::CPR) ^ G::kswz(rr)) * 8)) * uint32_t(sizeof(T));
+    dma_ov[q] = (uint32_t(lr) * uint32_t(a.sv_s) + uint32_t(((lane % G::CPR) ^ SW::swz(rr)) * 8)) * uint32_t(sizeof(T));
   }
   auto dma_mat = [&](auto isv_tag, int t, int ent, int buf) __attribute__((always_inline)) {
     constexpr bool ISV = decltype(isv_tag)::value;
@@ -1628,14 +1631,30 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     // the page's (and head's) first element, uniform
     const T* base = (ISV ? Vc : Kc) + (uint64_t(p) * uint32_t(ISV ? a.sv_b : a.sk_b) +
                                        uint64_t(uint32_t(g)) * uint32_t(ISV ? a.sv_h : a.sk_h));
+    const unsigned dst0 = lds0 + buf * G::TILEB + G::RPW * wave * G::ROWB;
+    // (temporal: a workgroup reads each K tile twice and neighbouring row
+    // blocks share tiles through L2; nt measured 5 % slower)
+    if (t * TILE + TILE <= seq_len) {  // uniform: a whole tile
+      const int key0 = t * TILE + G::RPW * wave;
+      const char* wbase = reinterpret_cast<const char*>(base + uint64_t(uint32_t(key0 & (a.page_size - 1))) * ss);
 #pragma unroll
-    for (int q = 0; q < G::NDMA; ++q) {
-      const int key = min(t * TILE + dma_rr[q], seq_len - 1);
-      const T* src = base + (uint64_t(uint32_t(key & (a.page_size - 1))) * ss + (ISV ? dma_cv[q] : dma_ck[q]));
-      const unsigned dst = lds0 + buf * G::TILEB + (G::RPW * wave + q * G::KPI) * G::ROWB;
-      // (temporal: a workgroup reads each K tile twice and neighbouring
-      // row blocks share tiles through L2; nt measured 5 % slower)
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)dst, 16, 0, 0);
+      for (int q = 0; q < G::NDMA; ++q)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(wbase + (ISV ? dma_ov[q] : dma_ok[q])),
+                                         (AttnLdsPtr)(uintptr_t)(dst0 + q * G::KPI * G::ROWB), 16, 0, 0);
+    } else {
+      // (the lane through an asm: per-lane values derived here stay here, not
+      // hoisted out of the loop to hold registers for the whole kernel)
+      int ln;
+      asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+#pragma unroll
+      for (int q = 0; q < G::NDMA; ++q) {
+        const int rr = G::RPW * wave + q * G::KPI + ln / G::CPR;
+        const int key = min(t * TILE + rr, seq_len - 1);
+        const uint32_t c = uint32_t(((ln % G::CPR) ^ (ISV ? SW::swz(rr) : G::kswz(rr))) * 8);
+        const T* src = base + (uint64_t(uint32_t(key & (a.page_size - 1))) * ss + c);
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (AttnLdsPtr)(uintptr_t)(dst0 + q * G::KPI * G::ROWB),
+                                         16, 0, 0);
+      }
     }
   };
   auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
@@ -2110,7 +2129,9 @@ template <int DT, int DMAX> bool dma_ok(const AttnArgs& a) {
   if constexpr (DT == FXPR_DTYPE_F32 || (DMAX != 64 && DMAX != 128)) {
     return false;
   } else {
-    return a.head_dim == DMAX && a.ps_shift >= 4;  // pages of 16, 32, ... keys
+    // pages of 16, 32, ... keys; key strides below 2^20 elements (the prefill
+    // kernel's 32-bit lane offsets span 16 of them)
+    return a.head_dim == DMAX && a.ps_shift >= 4 && a.sk_s < (int64_t(1) << 20) && a.sv_s < (int64_t(1) << 20);
   }
 }
 
