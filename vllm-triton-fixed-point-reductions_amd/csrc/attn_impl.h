@@ -1988,20 +1988,24 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
             // |acc| * 2^f below 2^22 (and the 16-bit range) for the whole
             // wave: fl(acc * 2^f + 1.5 * 2^23) is RNE(acc * 2^f) + 1.5 * 2^23
             // (exact product, one rounding, spacing 1, even constant), the
-            // bits quant gives; otherwise (large values, NaN) the exact path
-            if (__builtin_amdgcn_ballot_w64(!(vmax < vlim)) == 0) {
+            // bits quant gives. The terms go in unconditionally; if a lane is
+            // out of range (large values, NaN) the wave takes the same terms
+            // out again (sums wrap) and adds the exact ones. (A branch between
+            // the two updates left the sums in other registers on one side,
+            // and the loop copied all 32 back every tile.)
+            auto fast_term = [&](float x) { return __float_as_uint(__builtin_fmaf(x, a.fxp_scale, 12582912.0f)) - 0x4B400000u; };
+#pragma unroll
+            for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) wv[b][i] = static_cast<int32_t>(static_cast<uint32_t>(wv[b][i]) + fast_term(accv[b][i]));
+            if (__builtin_amdgcn_ballot_w64(!(vmax < vlim)) != 0) {
 #pragma unroll
               for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                  wv[b][i] = static_cast<int32_t>(static_cast<uint32_t>(wv[b][i]) +
-                                                  __float_as_uint(__builtin_fmaf(accv[b][i], a.fxp_scale, 12582912.0f)) -
-                                                  0x4B400000u);
-            } else {
-#pragma unroll
-              for (int b = 0; b < DBLK; ++b)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) wv[b][i] = wadd<BITS>(wv[b][i], quant<BITS>(__fmul_rn(accv[b][i], a.fxp_scale)));
+                for (int i = 0; i < 4; ++i) {
+                  const AccT undone = static_cast<int32_t>(static_cast<uint32_t>(wv[b][i]) - fast_term(accv[b][i]));
+                  wv[b][i] = wadd<BITS>(undone, quant<BITS>(__fmul_rn(accv[b][i], a.fxp_scale)));
+                }
             }
           }
         }
