@@ -1547,6 +1547,12 @@ __device__ __forceinline__ void lds_waitn_for(A& a, B& b, C& c, D& d) {
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
 }
 
+// 16 bytes per lane from a raw buffer at voff into LDS at dst + 16 * lane
+// (a helper: called directly in a kernel template, the builtin makes the
+// host pass drop the kernel's launch stub).
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, unsigned dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (AttnLdsPtr)(uintptr_t)dst, 16, voff, 0, 0, 0);
+}
 template <int OFF> __device__ __forceinline__ void lds_read_b128_off(unsigned addr, u32x4& x) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(addr), "n"(OFF) : "memory");
 }
@@ -1636,11 +1642,12 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     // blocks share tiles through L2; nt measured 5 % slower)
     if (t * TILE + TILE <= seq_len) {  // uniform: a whole tile
       const int key0 = t * TILE + G::RPW * wave;
-      const char* wbase = reinterpret_cast<const char*>(base + uint64_t(uint32_t(key0 & (a.page_size - 1))) * ss);
+      // a buffer based at the wave's first row: 32-bit lane offsets, no
+      // per-lane address math
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          uniform_ptr(base + uint64_t(uint32_t(key0 & (a.page_size - 1))) * ss), short(0), -1, kBufferDword3);
 #pragma unroll
-      for (int q = 0; q < G::NDMA; ++q)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(wbase + (ISV ? dma_ov[q] : dma_ok[q])),
-                                         (AttnLdsPtr)(uintptr_t)(dst0 + q * G::KPI * G::ROWB), 16, 0, 0);
+      for (int q = 0; q < G::NDMA; ++q) buffer_to_lds16(rs, dst0 + q * G::KPI * G::ROWB, ISV ? dma_ov[q] : dma_ok[q]);
     } else {
       // (the lane through an asm: per-lane values derived here stay here, not
       // hoisted out of the loop to hold registers for the whole kernel)

@@ -23,6 +23,17 @@ namespace fxpr {
 __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 __device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
 
+// Buffer resource word 3 for raw (unformatted, unswizzled) buffer access on
+// gfx9-family parts.
+constexpr int kBufferDword3 = 0x00020000;
+// A pointer the caller knows to be wave-uniform, as scalar registers (buffer
+// resources must be).
+template <typename T> __device__ __forceinline__ void* uniform_ptr(const T* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(u)), hi = __builtin_amdgcn_readfirstlane(uint32_t(u >> 32));
+  return reinterpret_cast<void*>((uint64_t(hi) << 32) | lo);
+}
+
 // ---------------------------------------------------------------------------
 // Storage types and conversions to / from fp32.
 

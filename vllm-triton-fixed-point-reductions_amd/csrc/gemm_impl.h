@@ -426,9 +426,6 @@ template <class BT> constexpr size_t big_lds_bytes() {
 }
 
 typedef __attribute__((address_space(3))) void* LdsPtr;
-// Buffer resource word 3 for raw (unformatted, unswizzled) buffer access on
-// gfx9-family parts.
-constexpr int kBufferDword3 = 0x00020000;
 // 16 bytes per lane from a raw buffer into LDS at dst + 16 * lane. (A helper:
 // called directly in a kernel template, the builtin makes the host pass drop
 // the kernel's launch stub.)
@@ -443,13 +440,6 @@ template <int N> __device__ __forceinline__ void lgkm_wait_for(u32x4& a) {
 template <int N>
 __device__ __forceinline__ void lgkm_wait_for(u32x4& a, u32x4& b, u32x4& c, u32x4& d, u32x4& e) {
   asm volatile("s_waitcnt lgkmcnt(%5)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e) : "n"(N) : "memory");
-}
-// A pointer the caller knows to be wave-uniform, as scalar registers (buffer
-// resources must be).
-template <typename T> __device__ __forceinline__ void* uniform_ptr(const T* p) {
-  const uint64_t u = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(u)), hi = __builtin_amdgcn_readfirstlane(uint32_t(u >> 32));
-  return reinterpret_cast<void*>((uint64_t(hi) << 32) | lo);
 }
 
 // WIDEN (BITS = 32, unsplit): the 64-bit accumulator semantics on 32-bit
