@@ -1547,6 +1547,12 @@ __device__ __forceinline__ void lds_waitn_for(A& a, B& b, C& c, D& d) {
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
 }
 
+// max(m, |x0|, |x1|, |x2|, |x3|), NaN-propagating
+__device__ __forceinline__ float absmax4(float m, const f32x4& x) {
+  return __builtin_elementwise_maximum(
+      m, __builtin_elementwise_maximum(__builtin_elementwise_maximum(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
+                                       __builtin_elementwise_maximum(__builtin_fabsf(x[2]), __builtin_fabsf(x[3]))));
+}
 // 16 bytes per lane from a raw buffer at voff into LDS at dst + 16 * lane
 // (a helper: called directly in a kernel template, the builtin makes the
 // host pass drop the kernel's launch stub).
@@ -1981,10 +1987,10 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
             }
             // lane: d = 16 db + 4 kg + e of its row
             if constexpr (FAST) {
+              // block db - 1's maximum while block db's MFMAs run (reading a
+              // result right after its MFMA costs wait states)
               accv[db] = acc;
-              vmax = __builtin_elementwise_maximum(
-                  vmax, __builtin_elementwise_maximum(__builtin_elementwise_maximum(__builtin_fabsf(acc[0]), __builtin_fabsf(acc[1])),
-                                                      __builtin_elementwise_maximum(__builtin_fabsf(acc[2]), __builtin_fabsf(acc[3]))));
+              if constexpr (db > 0) vmax = absmax4(vmax, accv[db - 1]);
             } else {
 #pragma unroll
               for (int i = 0; i < 4; ++i) wv[db][i] = wadd<BITS>(wv[db][i], quant<BITS>(__fmul_rn(acc[i], a.fxp_scale)));
@@ -1992,6 +1998,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
             __builtin_amdgcn_sched_barrier(0);
           });
           if constexpr (FAST) {
+            vmax = absmax4(vmax, accv[DBLK - 1]);
             // |acc| * 2^f below 2^22 (and the 16-bit range) for the whole
             // wave: fl(acc * 2^f + 1.5 * 2^23) is RNE(acc * 2^f) + 1.5 * 2^23
             // (exact product, one rounding, spacing 1, even constant), the
