@@ -1638,6 +1638,9 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   }
   auto dma_mat = [&](auto isv_tag, int t, int ent, int buf) __attribute__((always_inline)) {
     constexpr bool ISV = decltype(isv_tag)::value;
+    // (through the asm, nothing computed from the entry is hoisted to its
+    // load a step earlier, which would wait for the load there)
+    asm volatile("" : "+s"(ent));
     const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
     const uint32_t ss = uint32_t(ISV ? a.sv_s : a.sk_s);
     // the page's (and head's) first element, uniform
@@ -1685,8 +1688,8 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   auto live_lo = [&](int cc) { return max(cc * CT, t_lo); };
   auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
   int dcc = c_lo, dph = 0, didx = 0;  // DMA cursor
-  auto cur_tile = [&]() { return live_lo(dcc) + (dph ? (didx >> 1) : didx); };
-  auto cur_isv = [&]() { return dph == 1 && (didx & 1); };
+  auto cur_tile = [&]() { return live_lo(dcc) + (didx >> dph); };  // dph: 0 or 1
+  auto cur_isv = [&]() { return (dph & didx & 1) != 0; };
   auto advance = [&]() {
     const int nt = live_hi(dcc) - live_lo(dcc);
     if (++didx < (dph ? 2 * nt : nt)) return;
