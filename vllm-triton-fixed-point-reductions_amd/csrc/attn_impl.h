@@ -623,7 +623,7 @@ template <int DMAX> struct DmaGeom {
   static constexpr int KPI = 1024 / ROWB;        // key rows per wave instruction
   static constexpr int TILEB = TILE * ROWB;      // bytes per tile
   static constexpr int NDMA = TILEB / (kThreads * 16);  // DMA instructions per thread per tile
-  static constexpr int NS = 4;                   // LDS stages
+  static constexpr int NS = 4;                   // LDS stages (a power of two: stage index by mask)
   static __device__ __forceinline__ int swz(int r) {
     if constexpr (CPR >= 16) {
       return ((r & 3) << 2) | ((r >> 2) & 3);
@@ -958,11 +958,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
         dma_wait<NS - 2, G::NDMA>(total_steps - 1 - step);
         __builtin_amdgcn_s_barrier();
         if (step + NS - 1 < total_steps) {
-          dma_tile(dv, dt, dent, (step + NS - 1) % NS);
+          dma_tile(dv, dt, dent, (step + NS - 1) & (NS - 1));
           advance(dc_, dv, dt);
           dent = page_entry(dt);  // for the next step's DMAs
         }
-        const unsigned base = lds0 + (step % NS) * G::TILEB;
+        const unsigned base = lds0 + (step & (NS - 1)) * G::TILEB;
         ++step;
         return base;
       };
@@ -1505,6 +1505,7 @@ template <int DMAX> struct PDmaGeom {
   static constexpr int NDMA = RPW / KPI;             // DMA instructions per wave per tile
   static constexpr int NS = 4;                       // LDS stages (two workgroups per CU)
   static_assert(NDMA >= 1 && NDMA * KPI == RPW, "tile rows per wave");
+  static_assert((NS & (NS - 1)) == 0, "stage index by mask");
   // K tiles: the transposed score MFMAs read rows {0-3, 8-11, 16-19, 24-27}
   // (and the same + 4) of a 32-row group in one 16-lane read. Measured with
   // gfx950's LDS conflict counter on that exact pattern: 256-byte rows keep
@@ -1813,7 +1814,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       __builtin_amdgcn_s_barrier();
 #pragma unroll
       for (int u = 0; u < C; ++u) {
-        dma_tile(cur_isv(), cur_tile(), dent, (step + NS - 2 + u) % NS);
+        dma_tile(cur_isv(), cur_tile(), dent, (step + NS - 2 + u) & (NS - 1));
         advance();
         refresh_entry();
       }
@@ -1821,7 +1822,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       step += C;
       return e;
     };
-    auto stage_base = [&](int e) -> unsigned { return lds0 + (e % NS) * G::TILEB; };
+    auto stage_base = [&](int e) -> unsigned { return lds0 + (e & (NS - 1)) * G::TILEB; };
     // The four transposed score MFMA chains of the tile at base (q = 2 s + h),
     // software-pipelined: chain q + 1's fragment reads are issued before chain
     // q's wait and MFMAs (only the newest chain's QSTEPS reads may remain in
