@@ -1688,19 +1688,26 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   // exact. The first entries go out before the Q and row-setup loads.
   auto live_lo = [&](int cc) { return max(cc * CT, t_lo); };
   auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
-  int dcc = c_lo, dph = 0, didx = 0;  // DMA cursor
-  auto cur_tile = [&]() { return live_lo(dcc) + (didx >> dph); };  // dph: 0 or 1
+  // DMA cursor: chunk dcc (first live tile dlo), phase dph (0 or 1), entry
+  // didx of dlim in the phase; only a phase or chunk change recomputes the
+  // bounds (the common advance is an add and a compare)
+  int dcc = c_lo, dph = 0, didx = 0;
+  int dlo = live_lo(c_lo), dlim = live_hi(c_lo) - dlo;
+  auto cur_tile = [&]() { return dlo + (didx >> dph); };
   auto cur_isv = [&]() { return (dph & didx & 1) != 0; };
   auto advance = [&]() {
-    const int nt = live_hi(dcc) - live_lo(dcc);
-    if (++didx < (dph ? 2 * nt : nt)) return;
+    if (++didx < dlim) return;
+    const int nt = live_hi(dcc) - dlo;
     if (dph == 0) {
       dph = 1;
       didx = 0;
+      dlim = 2 * nt;
     } else if (dcc + 1 < c_hi) {
       ++dcc;
       dph = 0;
       didx = 0;
+      dlo = live_lo(dcc);
+      dlim = live_hi(dcc) - dlo;
     } else {
       didx = 2 * nt - 1;
     }
