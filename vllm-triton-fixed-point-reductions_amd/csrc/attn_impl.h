@@ -2038,7 +2038,18 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       // the chunk's denominator over the row's four lanes, then the fold
       den = wadd<BITS>(den, __shfl_xor(den, 16, 64));
       den = wadd<BITS>(den, __shfl_xor(den, 32, 64));
-      if (mx != -__builtin_inff()) {  // else no key of the row in this chunk
+      if (__builtin_amdgcn_ballot_w64(Mr != -__builtin_inff()) == 0) {
+        // no row of the wave has folded a chunk yet (W = D = 0, M = -inf):
+        // the fold gives the chunk's own sums (rescale(0, 0) + rescale(x, 1));
+        // a row without a key here has zero sums (its weights are 0 and a
+        // NaN product quantises to 0) and keeps M = -inf
+#pragma unroll
+        for (int b = 0; b < DBLK; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Wr[b][i] = wv[b][i];
+        Dr = den;
+        Mr = mx;
+      } else if (mx != -__builtin_inff()) {  // else no key of the row in this chunk
         float Mn, fa, fb;
         merge_factors(Mr, mx, Mn, fa, fb);
         // Mn is M or mc, so fa or fb is 2^0 = 1 unless both maxima are +inf
