@@ -111,6 +111,17 @@ def test_rms_norm_bit_exact(dtype, residual, scale, shape):
     _rms_check(x, w, r)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("residual", [False, True])
+def test_rms_norm_scalar_path_many_elements(dtype, residual):
+    # a hidden size that is not a multiple of 8 takes the one-element-per-lane
+    # kernel; 262K outputs put dozens of fp32 results on an f16 rounding
+    # midpoint, where converting the fp32 product (what the oracle does)
+    # differs from rounding the exact product x * inv * w to f16 in one step
+    x, w, r = _rms_case(dtype, (64, 4099), seed=23, residual=residual)
+    _rms_check(x, w, r)
+
+
 def _realistic_rows(H=4096, seed=0):
     """RMS 3, 5, 20, 100, 1e4 and 1e-3 rows, plus an N(0, 0.5) row with one
     channel at 1500 (residual-stream magnitudes where a Q16.16 int32 sum of

@@ -2091,12 +2091,17 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   }
 
   if (me.valid) {
+    // the row's 32 quotients over one denominator (in [1e-6, 2^31]; the
+    // numerators are fixed-point values below 2^31): by its rounded
+    // reciprocal, the same bits as div_rn
     const float den_f = fmaxf(acc_f32<BITS>(Dr, a.fxp_inv), 1.0e-6f);
+    const float rcp = div_rn(1.0f, den_f);
     T* orow = static_cast<T*>(a.o) + me.token * a.so_t + int64_t(me.head) * a.so_h;
 #pragma unroll
     for (int b = 0; b < DBLK; ++b)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) orow[b * 16 + 4 * kg + i] = Io<DT>::store(div_rn(acc_f32<BITS>(Wr[b][i], a.fxp_inv), den_f));
+      for (int i = 0; i < 4; ++i)
+        orow[b * 16 + 4 * kg + i] = Io<DT>::store(div_rn_by_recip(acc_f32<BITS>(Wr[b][i], a.fxp_inv), den_f, rcp));
   }
 }
 

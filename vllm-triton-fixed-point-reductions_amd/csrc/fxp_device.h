@@ -22,6 +22,20 @@ namespace fxpr {
 // the correctly rounded division.
 __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 __device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
+// RN(a / b) for many a over one b, from y = RN(1 / b) (div_rn(1, b)):
+// q0 = RN(a y) is within a few ulps of a / b, and each correction
+// q' = RN(q + RN(a - b q) y) (two FMAs) brings q to RN(a / b) once q is
+// within an ulp (Markstein's theorem); two corrections. Exact while a / b
+// and the residuals a - b q (about 2^-24 a) stay normal: a = 0 or
+// |a| in [2^-63, 2^31] with b in [1e-6, 2^31] (the attention outputs) keeps
+// every intermediate above 2^-100.
+__device__ __forceinline__ float div_rn_by_recip(float a, float b, float y) {
+  float q = __fmul_rn(a, y);
+  float r = __builtin_fmaf(-b, q, a);
+  q = __builtin_fmaf(r, y, q);
+  r = __builtin_fmaf(-b, q, a);
+  return __builtin_fmaf(r, y, q);
+}
 
 // Buffer resource word 3 for raw (unformatted, unswizzled) buffer access on
 // gfx9-family parts.
@@ -56,7 +70,12 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+// fp32 -> f16, round half to even, of the fp32 value: through the asm the
+// conversion cannot fuse with the multiply or FMA that produced f into one
+// v_fma_mix*_f16 (a single rounding of the exact product to f16, which
+// differs from rounding the fp32 result when that lands on an f16 midpoint).
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  asm volatile("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
