@@ -1560,6 +1560,14 @@ __device__ __forceinline__ float absmax4(float m, const f32x4& x) {
 __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, unsigned dst, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (AttnLdsPtr)(uintptr_t)dst, 16, voff, 0, 0, 0);
 }
+// The same with a scalar offset and an instruction offset OFF, which the
+// hardware adds to both the source address (base + voff + soff + OFF) and the
+// LDS destination (dst + OFF + 16 * lane): consecutive loads into one stage
+// share M0.
+template <int OFF>
+__device__ __forceinline__ void buffer_to_lds16_off(__amdgpu_buffer_rsrc_t r, unsigned dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (AttnLdsPtr)(uintptr_t)dst, 16, voff, soff, OFF, 0);
+}
 template <int OFF> __device__ __forceinline__ void lds_read_b128_off(unsigned addr, u32x4& x) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(addr), "n"(OFF) : "memory");
 }
@@ -1630,12 +1638,18 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   // a whole tile's sources are a uniform base (page, head, the wave's first
   // row) plus these offsets; the last, partial tile of a request clamps its
   // keys per lane instead. (The host keeps 16 key strides below 2^26 bytes.)
+  // Instruction q's LDS rows start q KPI ROWB = q KiB past the wave's first
+  // row: that goes in the instruction offset, which the source address takes
+  // too, so it is taken out of the lane offset here (q KPI key strides are
+  // at least q KiB).
   uint32_t dma_ok[G::NDMA], dma_ov[G::NDMA];
 #pragma unroll
   for (int q = 0; q < G::NDMA; ++q) {
     const int lr = q * G::KPI + lane / G::CPR, rr = G::RPW * wave + lr;
-    dma_ok[q] = (uint32_t(lr) * uint32_t(a.sk_s) + uint32_t(((lane % G::CPR) ^ G::kswz(rr)) * 8)) * uint32_t(sizeof(T));
-    dma_ov[q] = (uint32_t(lr) * uint32_t(a.sv_s) + uint32_t(((lane % G::CPR) ^ SW::swz(rr)) * 8)) * uint32_t(sizeof(T));
+    dma_ok[q] = (uint32_t(lr) * uint32_t(a.sk_s) + uint32_t(((lane % G::CPR) ^ G::kswz(rr)) * 8)) * uint32_t(sizeof(T)) -
+                uint32_t(q * G::KPI * G::ROWB);
+    dma_ov[q] = (uint32_t(lr) * uint32_t(a.sv_s) + uint32_t(((lane % G::CPR) ^ SW::swz(rr)) * 8)) * uint32_t(sizeof(T)) -
+                uint32_t(q * G::KPI * G::ROWB);
   }
   auto dma_mat = [&](auto isv_tag, int t, int ent, int buf) __attribute__((always_inline)) {
     constexpr bool ISV = decltype(isv_tag)::value;
@@ -1652,12 +1666,15 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     // blocks share tiles through L2; nt measured 5 % slower)
     if (t * TILE + TILE <= seq_len) {  // uniform: a whole tile
       const int key0 = t * TILE + G::RPW * wave;
-      // a buffer based at the wave's first row: 32-bit lane offsets, no
-      // per-lane address math
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          uniform_ptr(base + uint64_t(uint32_t(key0 & (a.page_size - 1))) * ss), short(0), -1, kBufferDword3);
-#pragma unroll
-      for (int q = 0; q < G::NDMA; ++q) buffer_to_lds16(rs, dst0 + q * G::KPI * G::ROWB, ISV ? dma_ov[q] : dma_ok[q]);
+      // a buffer based at the page's first row, the wave's first row in the
+      // scalar offset (the host keeps a page's bytes below 2^31): 32-bit
+      // lane offsets, no per-lane address math
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), short(0), -1, kBufferDword3);
+      const uint32_t soff = uint32_t(key0 & (a.page_size - 1)) * ss * uint32_t(sizeof(T));
+      static_for<G::NDMA>([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        buffer_to_lds16_off<q * G::KPI * G::ROWB>(rs, dst0, ISV ? dma_ov[q] : dma_ok[q], soff);
+      });
     } else {
       // (the lane through an asm: per-lane values derived here stay here, not
       // hoisted out of the loop to hold registers for the whole kernel)
@@ -1819,6 +1836,22 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
       // everyone's
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(G::NDMA * (NS - 2 - C)) : "memory");
       __builtin_amdgcn_s_barrier();
+      if constexpr (C == 2) {
+        // In phase 1 the cursor usually stands at a tile's K entry with its V
+        // entry next (a step consumes a K / V pair and the cursor runs two
+        // entries ahead): both from the one page entry, one cursor update
+        if (dph != 0 && (didx & 1) == 0 && didx + 1 < dlim) {  // uniform
+          const int t = cur_tile();
+          dma_mat(std::false_type{}, t, dent, (step + NS - 2) & (NS - 1));
+          dma_mat(std::true_type{}, t, dent, (step + NS - 1) & (NS - 1));
+          ++didx;  // the first advance(): no phase change by the test above
+          advance();
+          refresh_entry();
+          const int e = step;
+          step += C;
+          return e;
+        }
+      }
 #pragma unroll
       for (int u = 0; u < C; ++u) {
         dma_tile(cur_isv(), cur_tile(), dent, (step + NS - 2 + u) & (NS - 1));
@@ -2176,7 +2209,10 @@ template <int DT, int DMAX> bool dma_ok(const AttnArgs& a) {
   } else {
     // pages of 16, 32, ... keys; key strides below 2^20 elements (the prefill
     // kernel's 32-bit lane offsets span 16 of them)
-    return a.head_dim == DMAX && a.ps_shift >= 4 && a.sk_s < (int64_t(1) << 20) && a.sv_s < (int64_t(1) << 20);
+    // and a page's K and V rows below 2^31 bytes (the prefill kernel's scalar
+    // offset to a wave's first row)
+    return a.head_dim == DMAX && a.ps_shift >= 4 && a.sk_s < (int64_t(1) << 20) && a.sv_s < (int64_t(1) << 20) &&
+           a.ps_shift < 31 && ((a.sk_s > a.sv_s ? a.sk_s : a.sv_s) << a.ps_shift) < (int64_t(1) << 30);
   }
 }
 
