@@ -763,7 +763,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   constexpr int RF_OFF = PS_OFF + 2 * QROWS * VP * 2;
   constexpr int RI_OFF = RF_OFF + 4 * QROWS * 4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(smem_raw));
+  // The dynamic LDS starts where the static LDS ends, rounded up to its
+  // alignment: a constant (the address of smem_raw, cast from a generic
+  // pointer, comes back as a null test and a select at every use)
+  const unsigned lds0 = (__builtin_amdgcn_groupstaticsize() + 15u) & ~15u;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, kg = lane >> 4;
   const int g = blockIdx.x % a.num_kv_heads;
@@ -1587,7 +1590,10 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   constexpr int NS = G::NS;
   static_assert(TILE == QUNIT, "one quantised chain per tile");
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(smem_raw));
+  // The dynamic LDS starts where the static LDS ends, rounded up to its
+  // alignment: a constant (the address of smem_raw, cast from a generic
+  // pointer, comes back as a null test and a select at every use)
+  const unsigned lds0 = (__builtin_amdgcn_groupstaticsize() + 15u) & ~15u;
 
   const int tid = threadIdx.x, lane = tid & 63, kg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1664,7 +1670,7 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     const unsigned dst0 = lds0 + buf * G::TILEB + G::RPW * wave * G::ROWB;
     // (temporal: a workgroup reads each K tile twice and neighbouring row
     // blocks share tiles through L2; nt measured 5 % slower)
-    if (t * TILE + TILE <= seq_len) {  // uniform: a whole tile
+    if (t * TILE + TILE <= seq_len) {  // uniform: a whole tile  // uniform: a whole tile
       const int key0 = t * TILE + G::RPW * wave;
       // a buffer based at the page's first row, the wave's first row in the
       // scalar offset (the host keeps a page's bytes below 2^31): 32-bit
