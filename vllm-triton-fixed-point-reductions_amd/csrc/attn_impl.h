@@ -1631,7 +1631,10 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   auto page_entry = [&](int t) -> int {
     const int key0 = min(t * TILE + G::RPW * wave, seq_len - 1);
     const int lb = __builtin_amdgcn_readfirstlane(key0 >> a.ps_shift);
-    return bt_row[min(lb, a.max_blocks - 1)];
+    // (an unsigned index: a 32-bit scalar offset of the load, no 64-bit
+    // address arithmetic; key0 >= 0, as the kernel visits tiles only when
+    // seq_len >= 1)
+    return bt_row[uint32_t(min(lb, a.max_blocks - 1))];
   };
   // K and V tiles are separate compile-time instances behind a uniform
   // branch on isv (a select between the two matrices' fields becomes a load
@@ -1657,12 +1660,15 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
     dma_ov[q] = (uint32_t(lr) * uint32_t(a.sv_s) + uint32_t(((lane % G::CPR) ^ SW::swz(rr)) * 8)) * uint32_t(sizeof(T)) -
                 uint32_t(q * G::KPI * G::ROWB);
   }
-  auto dma_mat = [&](auto isv_tag, int t, int ent, int buf) __attribute__((always_inline)) {
-    constexpr bool ISV = decltype(isv_tag)::value;
-    // (through the asm, nothing computed from the entry is hoisted to its
-    // load a step earlier, which would wait for the load there)
+  // the page of a block-table entry (clamped into the cache). (Through the
+  // asm, nothing computed from the entry is hoisted to its load a step
+  // earlier, which would wait for the load there.)
+  auto page_of = [&](int ent) -> uint32_t {
     asm volatile("" : "+s"(ent));
-    const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
+    return uint32_t(ent < 0 ? 0 : min(ent, last_block));
+  };
+  auto dma_mat = [&](auto isv_tag, int t, uint32_t p, int buf) __attribute__((always_inline)) {
+    constexpr bool ISV = decltype(isv_tag)::value;
     const uint32_t ss = uint32_t(ISV ? a.sv_s : a.sk_s);
     // the page's (and head's) first element, uniform
     const T* base = (ISV ? Vc : Kc) + (uint64_t(p) * uint32_t(ISV ? a.sv_b : a.sk_b) +
@@ -1699,9 +1705,9 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
   };
   auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
     if (isv)
-      dma_mat(std::true_type{}, t, ent, buf);
+      dma_mat(std::true_type{}, t, page_of(ent), buf);
     else
-      dma_mat(std::false_type{}, t, ent, buf);
+      dma_mat(std::false_type{}, t, page_of(ent), buf);
   };
 
   // The tile stream: per chunk cc, its nt live K tiles (phase 0), then K and
@@ -1848,8 +1854,9 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
         // entries ahead): both from the one page entry, one cursor update
         if (dph != 0 && (didx & 1) == 0 && didx + 1 < dlim) {  // uniform
           const int t = cur_tile();
-          dma_mat(std::false_type{}, t, dent, (step + NS - 2) & (NS - 1));
-          dma_mat(std::true_type{}, t, dent, (step + NS - 1) & (NS - 1));
+          const uint32_t p = page_of(dent);
+          dma_mat(std::false_type{}, t, p, (step + NS - 2) & (NS - 1));
+          dma_mat(std::true_type{}, t, p, (step + NS - 1) & (NS - 1));
           ++didx;  // the first advance(): no phase change by the test above
           advance();
           refresh_entry();
