@@ -1571,6 +1571,9 @@ template <int OFF>
 __device__ __forceinline__ void buffer_to_lds16_off(__amdgpu_buffer_rsrc_t r, unsigned dst, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (AttnLdsPtr)(uintptr_t)dst, 16, voff, soff, OFF, 0);
 }
+template <int OFF> __device__ __forceinline__ void lds_read_b64_tr16_off(unsigned addr, uint64_t& x) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(x) : "v"(addr), "n"(OFF) : "memory");
+}
 template <int OFF> __device__ __forceinline__ void lds_read_b128_off(unsigned addr, u32x4& x) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(addr), "n"(OFF) : "memory");
 }
@@ -2014,12 +2017,19 @@ __global__ __launch_bounds__(kPThreads, 2) void attn_prefill_dma_kernel(AttnArgs
           // d blocks software-pipelined: block db + 1's V reads go out before
           // block db's wait (only they may remain in flight)
           uint64_t vr[2][NK0][2];
+          // (step s reads KI rows further on: voff0[s][h] = voff0[0][h] + s KI
+          // ROWB, as the swizzle takes row bits below 4 only; that goes in the
+          // read's offset field, one address per (h, d block))
           auto issue_v = [&](auto dbc) __attribute__((always_inline)) {
             constexpr int db = decltype(dbc)::value;
 #pragma unroll
-            for (int s = 0; s < NK0; ++s)
-#pragma unroll
-              for (int h = 0; h < 2; ++h) lds_read_b64_tr16(base + (voff0[s][h] ^ (db << 5)), vr[db & 1][s][h]);
+            for (int h = 0; h < 2; ++h) {
+              const unsigned va = base + (voff0[0][h] ^ (db << 5));
+              static_for<NK0>([&](auto sc) {
+                constexpr int s = decltype(sc)::value;
+                lds_read_b64_tr16_off<s * KI * G::ROWB>(va, vr[db & 1][s][h]);
+              });
+            }
           };
           issue_v(std::integral_constant<int, 0>{});
           f32x4 accv[DBLK];  // fast variant: the tile's weighted V, quantised after the range check
