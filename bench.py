@@ -6,11 +6,13 @@
 Prints ONE JSON line. The headline (`metric`/`value`) is BASELINE.json's
 metric: the fixed-point lm_head GEMM in TFLOP/s (bf16 A[8192,4096] x
 B[4096,128256], Q16.16 in int32) whose `roofline` is against the dense bf16
-MFMA peak; every other BASELINE configuration rides along under `extra`
-with its own roofline: the paged split-K decode attention at each split count
-(HBM GB/s), the other GEMM shapes, RMSNorm + residual and log-softmax (HBM),
-causal prefill attention (MFMA), config 1's cast / row-sum / RMSNorm chain,
-and config 5's Llama-3-8B-shaped decoder (tokens/s, report only). A step is one call of the workload's op on one batch of
+MFMA peak. The metric's second half, the paged split-K decode attention in
+HBM GB/s, is `decode` (automatic splits and each forced count). Every other
+BASELINE configuration rides along under `workloads` with its own roofline:
+the other GEMM shapes, RMSNorm + residual and log-softmax (HBM), causal
+prefill attention (MFMA), config 1's cast / row-sum / RMSNorm chain, and
+config 5's Llama-3-8B-shaped decoder (tokens/s at batch 32 / 8 / 1, report
+only). A step is one call of the workload's op on one batch of
 seeded synthetic input already resident in HBM; each workload times exactly K
 steps between HIP events recorded on the stream the kernels run on, after W
 warmup steps, with a device synchronize on both sides. Inputs whose total
@@ -341,75 +343,44 @@ def wl_config1(steps, warmup, int_bits=32):
             "ms": round(ms, 5), "bytes": nbytes, "roofline": hbm_roofline(nbytes, ms)}
 
 
-def wl_e2e_llama(steps, warmup, batch=32, prompt=2048):
+def wl_e2e_llama(batches=(32, 8, 1), prompt=2048, max_new=128):
     """BASELINE config 5 on the library's own harness (tests/e2e_decoder.py):
     a random-init Llama-3-8B-shaped decoder (32 layers, hidden 4096, 32/8
-    heads of 128, FFN 14336, vocab 128256, bf16 weights ~N(0, 0.02)) built
-    only from the fxpr ops, `batch` random-token prompts of `prompt` tokens
-    prefilled in one step, then greedy decode steps of the whole batch (the
-    sampler with top-5 log-probabilities). Reported: decode tokens/s (a step =
-    one decode token for every request) and the prefill's tokens/s."""
+    heads of 128, FFN 14336, vocab 128256, bf16 weights ~N(0, 0.02); merged
+    q/k/v and gate/up projections as vLLM holds them) built only from the
+    fxpr ops, served as vLLM serves it: `batch` random-token prompts of
+    `prompt` tokens prefilled in one eager step, one eager decode step, then
+    the remaining decode steps of the whole batch replayed from a captured
+    HIP graph (greedy sampler with top-5 log-probabilities), `max_new` new
+    tokens per request in all, at each batch size. Reported per batch size:
+    decode tokens/s over the replayed steps (a step = one token for every
+    request) and the prefill's tokens/s."""
     import torch
 
     sys.path.insert(0, str(ROOT / "tests"))
-    from e2e_decoder import Config, Decoder, Request
+    from e2e_decoder import Config, Decoder, run_graph
 
-    pages = batch * -(-(prompt + steps + warmup + 1) // 16) + 8
+    pages = max(batches) * -(-(prompt + max_new) // 16) + 8
     model = Decoder(Config.llama3_8b(pages), seed=0)
     g = torch.Generator("cpu").manual_seed(5)
-    prompts = [torch.randint(0, 128256, (prompt,), generator=g).tolist() for _ in range(batch)]
-    reqs = [Request(i, p, 1 << 30, tokens=list(p)) for i, p in enumerate(prompts)]
-    dev = "cuda"
-    free = list(range(pages))
-    max_pages = -(-(prompt + steps + warmup + 1) // 16)
-
-    def forward():
-        toks, pos, slots, qsl, sls, bts = [], [], [], [0], [], []
-        for rq in reqs:
-            new = rq.tokens[rq.cached:]
-            while len(rq.pages) < -(-len(rq.tokens) // 16):
-                rq.pages.append(free.pop(0))
-            for j, t in enumerate(new):
-                p = rq.cached + j
-                toks.append(t)
-                pos.append(p)
-                slots.append(rq.pages[p // 16] * 16 + p % 16)
-            qsl.append(qsl[-1] + len(new))
-            sls.append(len(rq.tokens))
-            bts.append(rq.pages + [0] * (max_pages - len(rq.pages)))
-        last = [qsl[i + 1] - 1 for i in range(len(reqs))]
-        ids = model.step(torch.tensor(toks, device=dev), torch.tensor(pos, device=dev),
-                         torch.tensor(qsl, dtype=torch.int32, device=dev),
-                         torch.tensor(sls, dtype=torch.int32, device=dev),
-                         torch.tensor(bts, dtype=torch.int32, device=dev),
-                         torch.tensor(slots, dtype=torch.int64, device=dev),
-                         max(qsl[i + 1] - qsl[i] for i in range(len(reqs))), torch.tensor(last, device=dev))[0].cpu()
-        for i, rq in enumerate(reqs):
-            rq.cached = len(rq.tokens)
-            rq.tokens.append(int(ids[i]))
-
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    forward()                      # prefill of every prompt
-    torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
-    for _ in range(warmup):
-        forward()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        forward()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    prompts = [torch.randint(0, 128256, (prompt,), generator=g).tolist() for _ in range(max(batches))]
+    per = {}
+    for b in batches:
+        t = {}
+        run_graph(model, prompts[:b], max_new, timing=t)
+        ms = t["decode_s"] * 1e3 / t["decode_steps"]
+        per[f"batch{b}"] = {"decode_ms_per_step": round(ms, 4),
+                            "decode_tokens_per_s": round(b * t["decode_steps"] / t["decode_s"], 1),
+                            "prefill_tokens_per_s": round(b * prompt / t["prefill_s"], 1)}
+        log(f"  config 5 batch {b}: {per[f'batch{b}']}")
     del model
     torch.cuda.empty_cache()
-    return {"workload": f"config 5: Llama-3-8B-shaped decoder on the fxpr ops, batch {batch}, prompts {prompt}, "
-                        f"greedy decode (top-5 log-probs)",
-            "ms": round(ms, 5), "decode_tokens_per_s": round(batch / (ms * 1e-3), 1),
-            "prefill_tokens_per_s": round(batch * prompt / prefill_s, 1),
-            "roofline": {"bound": "mixed", "achieved": round(batch / (ms * 1e-3), 1), "peak": None,
+    head = per[f"batch{max(batches)}"]
+    return {"workload": f"config 5: Llama-3-8B-shaped decoder on the fxpr ops, prompts {prompt}, greedy "
+                        f"{max_new} new tokens (top-5 log-probs), decode from a captured HIP graph, "
+                        f"batch {'/'.join(str(b) for b in batches)}",
+            "ms": head["decode_ms_per_step"], "per_batch": per,
+            "roofline": {"bound": "mixed", "achieved": head["decode_tokens_per_s"], "peak": None,
                          "unit": "tokens/s", "frac": None, "traffic": None}}
 
 
@@ -426,6 +397,7 @@ def wl_hbm_copy(steps, warmup, nbytes=1 << 30):
 
 
 WORKLOADS = {
+    "gemm_lm_head": lambda s, w: wl_gemm(s, w, 8192),
     "decode_attn": lambda s, w: wl_decode(s, w, 0),
     "decode_attn_s1": lambda s, w: wl_decode(s, w, 1),
     "decode_attn_s2": lambda s, w: wl_decode(s, w, 2),
@@ -433,7 +405,6 @@ WORKLOADS = {
     "decode_attn_s8": lambda s, w: wl_decode(s, w, 8),
     "decode_attn_s16": lambda s, w: wl_decode(s, w, 16),
     "prefill_attn": lambda s, w: wl_prefill(s, w),
-    "gemm_lm_head": lambda s, w: wl_gemm(s, w, 8192),
     "gemm_lm_head_m2048": lambda s, w: wl_gemm(s, w, 2048),
     "gemm_lm_head_m256": lambda s, w: wl_gemm(s, w, 256),
     "gemm_lm_head_m32": lambda s, w: wl_gemm(s, w, 32),
@@ -446,7 +417,7 @@ WORKLOADS = {
     "log_softmax_f32out_q32i64": lambda s, w: wl_log_softmax(s, w, 64, 32, fp32_out=True),
     "config1_q16_i32": lambda s, w: wl_config1(s, w, 32),
     "config1_q16_i64": lambda s, w: wl_config1(s, w, 64),
-    "e2e_llama3_8b": lambda s, w: wl_e2e_llama(min(s, 8), 2),
+    "e2e_llama3_8b": lambda s, w: wl_e2e_llama(),
     "hbm_copy": lambda s, w: wl_hbm_copy(s, w),
 }
 HEADLINE_ORDER = ["gemm_lm_head", "decode_attn", "rms_norm"]
@@ -455,11 +426,10 @@ HEADLINE_ORDER = ["gemm_lm_head", "decode_attn", "rms_norm"]
 # ---------------------------------------------------------------------------
 # CPU baseline: the CPU emulation of the same fixed-point path, timed per
 # BASELINE configuration on this box's host cores. GEMM, RMSNorm,
-# log-softmax and the casts run as PyTorch CPU code on every host thread
-# (oracle/torch_cpu.py, pinned bit for bit to the numpy oracle); the decode
-# attention runs as the numpy oracle (oracle/attention.py, one core). Shapes
-# too slow to run whole are timed on a documented sample and extrapolated
-# linearly in the sampled dimension; each entry says which.
+# log-softmax, the casts and the decode attention run as PyTorch CPU code on
+# every host thread (oracle/torch_cpu.py, pinned bit for bit to the numpy
+# oracle). Shapes too slow to run whole are timed on a documented sample and
+# extrapolated linearly in the sampled dimension; each entry says which.
 
 
 def _timed(fn, min_s: float = 0.0):
@@ -475,11 +445,8 @@ def _timed(fn, min_s: float = 0.0):
 def cpu_suite(scale: float = 1.0) -> dict:
     """Per-configuration CPU timings. `scale` multiplies the sample sizes of
     the extrapolated entries (1.0: about a minute in all)."""
-    import numpy as np
     import torch
 
-    from oracle import attention as OA
-    from oracle import numerics as ON
     from oracle import torch_cpu as TC
 
     threads = os.cpu_count() or 1
@@ -556,25 +523,22 @@ def cpu_suite(scale: float = 1.0) -> dict:
                                                 f"A[{M},{K}] x B[{K},{nc}] of N={N2}, Q16.16 in int32", True)
 
     # config 4: decode attention, 64 one-token requests with the GPU bench's
-    # seeded context lengths U[512, 8192], 16-token pages, whole (numpy oracle)
+    # seeded context lengths U[512, 8192], 16-token pages, whole (the chunked
+    # algorithm as PyTorch CPU code on every host thread)
     gl = torch.Generator("cpu").manual_seed(0)
-    sl = torch.randint(512, 8193, (64,), generator=gl, dtype=torch.int32).numpy()
+    sl = torch.randint(512, 8193, (64,), generator=gl, dtype=torch.int32)
     nbk = [-(-int(L) // 16) for L in sl]
-    rng = np.random.default_rng(0)
-    kv = ON.store(rng.standard_normal((sum(nbk), 2, 16, 8, 128)).astype(np.float32), "bf16")
-    bt = np.zeros((64, max(nbk)), np.int32)
+    kv = bf16(randn(sum(nbk), 2, 16, 8, 128))
+    bt = torch.zeros(64, max(nbk), dtype=torch.int32)
     off = 0
     for i, nb in enumerate(nbk):
-        bt[i, :nb] = np.arange(off, off + nb)
+        bt[i, :nb] = torch.arange(off, off + nb, dtype=torch.int32)
         off += nb
-    q = ON.store(rng.standard_normal((64, 32, 128)).astype(np.float32), "bf16")
-    qsl = np.arange(65, dtype=np.int32)
-    dt, _ = _timed(lambda: OA.unified_attention(q, kv, qsl, sl, bt, "bf16", softmax_scale=128 ** -0.5,
-                                                chunk_keys=OA.CHUNK_KEYS))
+    q = bf16(randn(64, 32, 128))
+    dt, _ = _timed(lambda: TC.decode_attention(q, kv, sl, bt, "bf16", 128 ** -0.5, 32, 16))
     nbytes = int(sl.sum()) * 4096 + 2 * 64 * 32 * 128 * 2
-    out["config4_decode_attention"] = entry(nbytes / dt / 1e9, "GB/s", dt, 1,
-                                            f"full: 64 requests, sum of contexts {int(sl.sum())}",
-                                            impl="numpy oracle")
+    out["config4_decode_attention"] = entry(nbytes / dt / 1e9, "GB/s", dt, threads,
+                                            f"full: 64 requests, sum of contexts {int(sl.sum())}, Q16.16/i32")
     return out
 
 
@@ -644,18 +608,36 @@ def main() -> None:
         "data": "synthetic (seeded torch CPU generator, copied to HBM)",
         "config": {"workload": head["workload"], "headline": headline},
         "roofline": rf,
-        "extra": {k: v for k, v in results.items() if k != headline},
-        "host": {"cpu_count": os.cpu_count(), "cpu_model": cpu_model(),
-                 "torch_threads": torch.get_num_threads(),
-                 "gpu": torch.cuda.get_device_name(0)},
     }
+    # the metric's second half: paged split-K decode attention (HBM)
+    dec = {k: v for k, v in results.items() if k.startswith("decode_attn")}
+    if dec:
+        out["decode"] = {("auto" if k == "decode_attn" else k.split("_")[-1]): compact(v) for k, v in dec.items()}
     if not args.no_cpu:
         log("cpu baseline (oracle per configuration) ...")
         suite = cpu_suite(args.cpu_scale)
         out["cpu_baseline"] = cpu_baseline_from(suite, headline)
-        out["cpu_suite"] = suite
+        out["cpu_suite"] = {k: {kk: v[kk] for kk in ("value", "unit", "cores", "sample", "extrapolated")}
+                            for k, v in suite.items()}
         log(f"  {json.dumps(suite)}")
+    out["workloads"] = {k: compact(v) for k, v in results.items() if k != headline}
+    out["host"] = {"cpu_count": os.cpu_count(), "cpu_model": cpu_model(),
+                   "torch_threads": torch.get_num_threads(), "gpu": torch.cuda.get_device_name(0)}
     print(json.dumps(out), flush=True)
+
+
+def compact(r: dict) -> dict:
+    """A workload's result for the JSON line: what ran, ms per step and its
+    roofline (achieved, unit, fraction of peak, measured HBM traffic)."""
+    rf = r["roofline"]
+    c = {"workload": r["workload"], "ms": r["ms"], "achieved": rf["achieved"], "unit": rf["unit"],
+         "frac": rf["frac"], "bound": rf["bound"]}
+    if rf.get("traffic") is not None:
+        c["traffic"] = rf["traffic"]
+    for k in ("splits", "per_batch"):
+        if k in r:
+            c[k] = r[k]
+    return c
 
 
 if __name__ == "__main__":

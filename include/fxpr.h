@@ -43,7 +43,8 @@ enum {
   FXPR_E_BITS = -2,      /* int_bits / frac_bits / float_bits out of range */
   FXPR_E_SHAPE = -3,     /* negative or inconsistent sizes */
   FXPR_E_WORKSPACE = -4, /* workspace missing or smaller than required */
-  FXPR_E_ARG = -5        /* any other invalid argument */
+  FXPR_E_ARG = -5,       /* any other invalid argument */
+  FXPR_E_CAPTURE = -6    /* set-up that cannot run while the stream is capturing */
 };
 
 /* Text for a return code of any entry point (static storage). */
@@ -115,6 +116,22 @@ int fxpr_rms_norm(const void* x, void* residual, const void* weight, void* y,
 int fxpr_log_softmax(const void* x, int x_dtype, void* y, int y_dtype,
                      int64_t rows, int64_t cols, int int_bits, int frac_bits,
                      void* stream);
+
+/*
+ * Test hooks of fxpr_log_softmax's split-row kernel (no counterpart in the
+ * reference). The kernel's workgroups of one row exchange their span maxima,
+ * then their exact span sums, through device memory, polling each exchange
+ * at most a number of times (fxpr_debug_lsm_default_spin_limit(): 16384,
+ * milliseconds) before a workgroup computes what it waits for (the row's
+ * maximum and exact sum) itself from the input, which gives the same bits.
+ * fxpr_debug_set_lsm_spin_limit sets the two limits for later launches of
+ * this process (0: that poll gives up at once, forcing its path);
+ * fxpr_debug_lsm_fallbacks reads, synchronously, how many workgroups on the
+ * current device have taken such a path so far.
+ */
+int fxpr_debug_set_lsm_spin_limit(int max_tries, int sum_tries);
+int fxpr_debug_lsm_default_spin_limit(void);
+int fxpr_debug_lsm_fallbacks(unsigned long long* count);
 
 /*
  * Deterministic greedy sampling with log-probabilities over contiguous
@@ -213,7 +230,10 @@ int fxpr_unified_attention(
  * fxpr_unified_attention without the workspace arguments: allocates nothing.
  * The split partials go to a static device array of FXPR_STATIC_SCRATCH_BYTES
  * per GPU; a launch whose fxpr_attention_workspace_bytes() exceeds that is
- * rejected with FXPR_E_WORKSPACE before anything runs. Same results as
+ * rejected with FXPR_E_WORKSPACE before anything runs. The array's device
+ * address is looked up at the first split call on each device, which must
+ * not be under HIP graph capture (FXPR_E_CAPTURE; any eager call that splits
+ * sets it up, and capture is fine after that). Same results as
  * fxpr_unified_attention bit for bit. Calls that overlap on one GPU (two
  * streams, or two host threads) share the array and race: serialise them.
  * The stream must belong to the current device or be NULL.

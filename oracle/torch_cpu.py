@@ -1,8 +1,9 @@
-"""The oracle's fixed-point GEMM, RMSNorm, log-softmax and casts as PyTorch
-CPU code (multi-threaded), for the benchmark's CPU baseline.
+"""The oracle's fixed-point GEMM, RMSNorm, log-softmax, casts and decode
+attention as PyTorch CPU code (multi-threaded), for the benchmark's CPU
+baseline.
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). The same arithmetic as
-oracle.gemm / oracle.rows / oracle.numerics, step for step: fp32 values
+oracle.gemm / oracle.rows / oracle.numerics / oracle.attention, step for step: fp32 values
 held in torch.float32 (one IEEE rounding per operation), float64 tile dots
 rounded once to fp32, integers in int64; tests/test_oracle_torch_cpu.py pins
 every function bit for bit against the numpy restatement. Storage
@@ -177,3 +178,76 @@ def log_softmax(x, io_in: str, io_out: str, int_bits: int, frac_bits: int) -> to
                       log_own(torch.where(total == 0, torch.ones_like(S), S)))
     lse = m + lnS
     return store(xf - lse[:, None], io_out).reshape(x.shape)
+
+
+def _wrap(v: torch.Tensor, int_bits: int) -> torch.Tensor:
+    if int_bits == 64:
+        return v
+    m, h = 1 << int_bits, 1 << (int_bits - 1)
+    return torch.remainder(v + h, m) - h
+
+
+def _rescale(x: torch.Tensor, f: torch.Tensor, int_bits: int) -> torch.Tensor:
+    """oracle.attention._rescale: RNE(fl64(x) * fl64(f)), saturated."""
+    r = torch.round(_wrap(x, int_bits).to(F64) * f.to(F64))
+    lim = 2.0 ** (int_bits - 1)
+    r = torch.where(r >= lim, torch.full_like(r, lim - 1), torch.where(r < -lim, torch.full_like(r, -lim), r))
+    return r.to(I64)
+
+
+def decode_attention(q, kv_cache, seq_lens, block_table, io: str, softmax_scale: float,
+                     int_bits: int, frac_bits: int, chunk_keys: int = 512) -> torch.Tensor:
+    """oracle.attention.unified_attention(chunk_keys=512) for decode batches:
+    one query per request (query_start_loc = arange(R + 1)), causal, no
+    window, softcap or ALiBi, all heads of a request at once. q [R, Hq, D];
+    kv_cache [NB, 2, page, Hkv, D]; returns o [R, Hq, D] in storage form."""
+    qf = load(q, io).to(F64)
+    kv = load(kv_cache, io)
+    R, Hq, D = qf.shape
+    _, _, ps, Hkv, _ = kv.shape
+    G = Hq // Hkv
+    bn = 32 if io == "f32" else 64
+    ss_log2 = torch.tensor(float(softmax_scale) * 1.4426950408889634, dtype=F32)
+    scale = torch.tensor(2.0 ** frac_bits, dtype=F32)
+    out = torch.zeros(R, Hq, D, dtype=F32)
+    for r in range(R):
+        L = int(seq_lens[r])
+        nblk = -(-L // ps)
+        blocks = block_table[r, :nblk].long()
+        K = kv[blocks, 0].reshape(nblk * ps, Hkv, D)[:L].to(F64)
+        Lp = -(-L // bn) * bn
+        V = torch.zeros(Lp, Hkv, D, dtype=F64)
+        V[:L] = kv[blocks, 1].reshape(nblk * ps, Hkv, D)[:L]
+        qh = qf[r].reshape(Hkv, G, D)
+        s = torch.full((Hkv, G, Lp), float("-inf"), dtype=F32)
+        s[:, :, :L] = torch.matmul(qh, K.permute(1, 2, 0)).to(F32) * ss_log2
+        M = torch.full((Hkv, G), float("-inf"), dtype=F32)
+        Dn = torch.zeros(Hkv, G, dtype=I64)
+        W = torch.zeros(Hkv, G, D, dtype=I64)
+        for k0 in range(0, Lp, chunk_keys):
+            k1 = min(Lp, k0 + chunk_keys)
+            sc = s[:, :, k0:k1]
+            m_raw = sc.amax(-1)
+            m = torch.where(torch.isfinite(m_raw), m_raw, torch.zeros_like(m_raw))
+            w = (sc - m[..., None]).to(F64).exp2().to(F32)
+            den = _wrap(rne_sat(w * scale, int_bits).sum(-1), int_bits)
+            p = load(store(w, io), io).to(F64)
+            nt = (k1 - k0) // bn
+            pv = torch.matmul(p.reshape(Hkv, G, nt, bn).permute(0, 2, 1, 3),
+                              V[k0:k1].reshape(nt, bn, Hkv, D).permute(2, 0, 1, 3)).to(F32)
+            wv = _wrap(rne_sat(pv * scale, int_bits).sum(1), int_bits)
+            # merge_chunk: fold the chunk into the running state
+            live = torch.isfinite(m_raw)
+            Mn = torch.where(live, torch.maximum(M, m_raw), M)
+            fa = torch.where(live, (M - Mn).to(F64).exp2(), torch.ones_like(M, dtype=F64)).to(F32)
+            fb = torch.where(live, (m_raw - Mn).to(F64).exp2(), torch.zeros_like(M, dtype=F64)).to(F32)
+            fa = torch.where(torch.isnan(fa), torch.zeros_like(fa), fa)
+            fb = torch.where(torch.isnan(fb), torch.zeros_like(fb), fb)
+            Dnn = _wrap(_rescale(Dn, fa, int_bits) + _rescale(den, fb, int_bits), int_bits)
+            Wn = _wrap(_rescale(W, fa[..., None], int_bits) + _rescale(wv, fb[..., None], int_bits), int_bits)
+            M = torch.where(live, Mn, M)
+            Dn = torch.where(live, Dnn, Dn)
+            W = torch.where(live[..., None], Wn, W)
+        den_f = torch.maximum(fixed_to_f32(Dn, frac_bits), torch.tensor(1e-6, dtype=F32))
+        out[r] = (fixed_to_f32(W, frac_bits) / den_f[..., None]).reshape(Hq, D)
+    return store(out, io)

@@ -1,7 +1,8 @@
 """A random-init Llama-shaped decoder built only from torch.ops.fxpr.* (test
-harness): embedding -> [RMSNorm -> q/k/v GEMMs -> RoPE -> KV-cache write ->
-paged attention -> o GEMM -> residual RMSNorm -> gate/up GEMMs -> SiLU * up ->
-down GEMM] x L -> final RMSNorm -> lm_head GEMM (each request's last token) ->
+harness): embedding -> [RMSNorm -> merged q/k/v GEMM -> RoPE -> KV-cache
+write -> paged attention -> o GEMM -> residual RMSNorm -> merged gate/up GEMM
+-> SiLU * up -> down GEMM] x L -> final RMSNorm -> lm_head GEMM (each
+request's last token) ->
 greedy sampler with top-k log-probabilities (sample_greedy_fxp), plus the full
 fixed-point log-probability row (log_softmax_fxp) when asked.
 
@@ -12,7 +13,10 @@ whether they are prefilling or decoding. The continuous-batching scheduler
 here runs any mix of prefills and decodes in one flat token batch, like
 vLLM's. Config() is a small model; Config.llama3_8b() is BASELINE config 5's
 shape (32 layers, hidden 4096, 32 / 8 heads of 128, FFN 14336, vocab 128256).
-Weights are drawn on the device from a seeded generator.
+The q/k/v and gate/up projections are one weight each ([(Hq + 2 Hkv) D, hidden]
+and [2 FFN, hidden]), as vLLM's QKVParallelLinear and MergedColumnParallelLinear
+hold them, so a layer runs four GEMMs (N = 6144, 4096, 28672, 4096 at the
+Llama-3-8B shape). Weights are drawn on the device from a seeded generator.
 """
 
 from __future__ import annotations
@@ -60,10 +64,10 @@ class Decoder:
         for _ in range(c.layers):
             self.layers.append({
                 "ln1": w(c.hidden, std=0.1, mean=1.0),
-                "wq": w(c.heads * c.head_dim, c.hidden), "wk": w(c.kv_heads * c.head_dim, c.hidden),
-                "wv": w(c.kv_heads * c.head_dim, c.hidden), "wo": w(c.hidden, c.heads * c.head_dim),
+                "wqkv": w((c.heads + 2 * c.kv_heads) * c.head_dim, c.hidden),
+                "wo": w(c.hidden, c.heads * c.head_dim),
                 "ln2": w(c.hidden, std=0.1, mean=1.0),
-                "wg": w(c.ffn, c.hidden), "wu": w(c.ffn, c.hidden), "wd": w(c.hidden, c.ffn),
+                "wgu": w(2 * c.ffn, c.hidden), "wd": w(c.hidden, c.ffn),
             })
         self.ln_f = w(c.hidden, std=0.1, mean=1.0)
         self.lm_head = w(c.vocab, c.hidden)
@@ -102,20 +106,23 @@ class Decoder:
                 x = torch.ops.fxpr.rms_norm_fxp(h, L["ln1"], c.eps)
             else:
                 x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, L["ln1"], c.eps)
-            q = self._rope(self._gemm(x, L["wq"]).view(T, c.heads, c.head_dim), positions)
-            k = self._rope(self._gemm(x, L["wk"]).view(T, c.kv_heads, c.head_dim), positions)
-            v = self._gemm(x, L["wv"]).view(T, c.kv_heads, c.head_dim)
+            qkv = self._gemm(x, L["wqkv"])
+            nq, nkv = c.heads * c.head_dim, c.kv_heads * c.head_dim
+            q = self._rope(qkv[:, :nq].view(T, c.heads, c.head_dim), positions)
+            k = self._rope(qkv[:, nq:nq + nkv].view(T, c.kv_heads, c.head_dim), positions)
+            v = qkv[:, nq + nkv:].view(T, c.kv_heads, c.head_dim)
             torch.ops.fxpr.reshape_and_cache(k, v, self.kv[li], slots)
             o = torch.empty_like(q)
             torch.ops.fxpr.unified_attention_fxp(q, self.kv[li], o, qsl, seq_lens, block_table, max_q, None,
                                                  True, c.head_dim ** -0.5, c.int_bits, c.frac_bits, 0.0, 0, 0)
-            del q, k, v
+            del q, k, v, qkv
             h = self._gemm(o.view(T, -1), L["wo"])
             x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, L["ln2"], c.eps)
-            act = torch.nn.functional.silu(self._gemm(x, L["wg"]).float())
-            act.mul_(self._gemm(x, L["wu"]).float())
+            gu = self._gemm(x, L["wgu"])
+            act = torch.nn.functional.silu(gu[:, :c.ffn].float())
+            act.mul_(gu[:, c.ffn:].float())
             h = self._gemm(act.to(c.dtype), L["wd"])
-            del act
+            del act, gu
         x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, self.ln_f, c.eps)
         logits = self._gemm(x[sample_rows].contiguous(), self.lm_head)
         ids, lp, top, top_lp = torch.ops.fxpr.sample_greedy_fxp(logits, c.num_logprobs, c.int_bits, c.frac_bits)
@@ -189,4 +196,107 @@ def run(model: Decoder, prompts: list[list[int]], max_new: int, schedule) -> dic
                 r.full.append(full[i])
             r.cached = len(r.tokens)
             r.tokens.append(int(ids[i]))
+    return reqs
+
+
+def run_graph(model: Decoder, prompts: list[list[int]], max_new: int, timing: dict | None = None) -> dict[int, Request]:
+    """Greedy generation as a serving loop runs it: every prompt prefilled in
+    one flat eager step, one eager decode step (which also settles the
+    allocator and first-launch set-up), then the remaining decode steps
+    replayed from one captured HIP graph, as vLLM serves decode batches. A
+    replay decodes one token for every request and advances the decode state
+    on the device (next token, position, context length, cache slot), so the
+    replays queue back to back with no host synchronisation. Each request
+    gets the pages for its prompt and all its new tokens up front. Returns
+    the requests as run() does (the bits must match it: no op's result depends
+    on page placement or on graph replay). If `timing` is a dict it receives
+    `prefill_s`, and `decode_s` / `decode_steps` for the replayed steps
+    (device-synchronised wall time)."""
+    import time
+
+    c, dev = model.cfg, model.dev
+    model.reset_cache()
+    B = len(prompts)
+    reqs = {i: Request(i, p, max_new, tokens=list(p)) for i, p in enumerate(prompts)}
+    max_pages = -(-max(len(p) + max_new for p in prompts) // c.page)
+    nxt = 0
+    for r in reqs.values():
+        need = -(-(len(r.prompt) + max_new) // c.page)
+        r.pages = list(range(nxt, nxt + need))
+        nxt += need
+    if nxt > c.pages:
+        raise ValueError(f"run_graph: {nxt} pages needed, the cache holds {c.pages}")
+    toks, pos, slots, qsl = [], [], [], [0]
+    for r in reqs.values():
+        for p, t in enumerate(r.prompt):
+            toks.append(t)
+            pos.append(p)
+            slots.append(r.pages[p // c.page] * c.page + p % c.page)
+        qsl.append(qsl[-1] + len(r.prompt))
+    bt = torch.tensor([r.pages + [0] * (max_pages - len(r.pages)) for r in reqs.values()],
+                      dtype=torch.int32, device=dev)
+    plen = torch.tensor([len(r.prompt) for r in reqs.values()], dtype=torch.int32, device=dev)
+    hist = []   # per step: (ids, log-prob, top-k ids, top-k log-probs, full row or None), on the device
+
+    def keep(out):
+        hist.append(tuple(None if o is None else o.clone() for o in out))
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = model.step(torch.tensor(toks, device=dev), torch.tensor(pos, device=dev),
+                     torch.tensor(qsl, dtype=torch.int32, device=dev), plen, bt,
+                     torch.tensor(slots, dtype=torch.int64, device=dev), max(len(p) for p in prompts),
+                     torch.tensor(qsl[1:], device=dev) - 1)
+    keep(out)
+    torch.cuda.synchronize()
+    if timing is not None:
+        timing["prefill_s"] = time.perf_counter() - t0
+
+    tok_d = out[0].clone()
+    pos_d = plen.to(torch.int64)          # position of the token fed in
+    sl_d = plen + 1                       # context length including it
+    slot_d = torch.empty(B, dtype=torch.int64, device=dev)
+    qsl_d = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    rows = torch.arange(B, device=dev)
+
+    def body():
+        slot_d.copy_(bt[rows, pos_d // c.page].to(torch.int64) * c.page + pos_d % c.page)
+        o = model.step(tok_d, pos_d, qsl_d, sl_d, bt, slot_d, 1, rows)
+        tok_d.copy_(o[0])
+        pos_d.add_(1)
+        sl_d.add_(1)
+        return o
+
+    if max_new >= 2:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):      # the first decode step, eager
+            keep(body())
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+    if max_new >= 3:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gout = body()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(max_new - 2):
+            graph.replay()
+            keep(gout)
+        torch.cuda.synchronize()
+        if timing is not None:
+            timing["decode_s"] = time.perf_counter() - t0
+            timing["decode_steps"] = max_new - 2
+        del graph, gout
+    for s, (ids, lp, top, top_lp, full) in enumerate(hist):
+        ids, lp, top, top_lp = ids.cpu(), lp.cpu(), top.cpu(), top_lp.cpu()
+        full = None if full is None else full.cpu()
+        for i, r in enumerate(reqs.values()):
+            r.logprobs.append(lp[i])
+            r.topk.append((top[i], top_lp[i]))
+            if full is not None:
+                r.full.append(full[i])
+            r.tokens.append(int(ids[i]))
+    for r in reqs.values():
+        r.cached = len(r.tokens) - 1
     return reqs

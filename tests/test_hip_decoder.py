@@ -14,7 +14,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from e2e_decoder import Config, Decoder, run
+from e2e_decoder import Config, Decoder, run, run_graph
 
 pytestmark = pytest.mark.gpu
 
@@ -72,6 +72,19 @@ def test_batch_1_vs_8_vs_mixed():
             assert tok == int(torch.argmax(row)) and torch.equal(_bits(row[tok]), _bits(r.logprobs[s]))
 
 
+def test_graph_decode_matches_eager():
+    # the serving loop the bench times: decode steps replayed from one
+    # captured graph, state advanced on the device, pages assigned up front
+    import fxpr_vllm  # noqa: F401
+
+    model = Decoder(Config())
+    prompts = _prompts(8, seed=3)
+    ref = run(model, prompts, 6, _all)
+    got = run_graph(model, prompts, 6)
+    for rid in ref:
+        _assert_same(ref[rid], got[rid], f"graph request {rid}")
+
+
 def test_batch_32_matches_batch_1_subset():
     import fxpr_vllm  # noqa: F401
 
@@ -84,7 +97,7 @@ def test_batch_32_matches_batch_1_subset():
 
 # --- the Llama-3-8B shape --------------------------------
 
-PROMPT_LEN, BATCH, MAX_NEW = 2048, 32, 16
+PROMPT_LEN, BATCH, MAX_NEW = 2048, 32, 128
 
 
 @pytest.fixture(scope="module")
@@ -100,9 +113,10 @@ def llama3_8b():
 
 
 def test_llama3_8b_shape_batch_1_8_32(llama3_8b):
-    # 32 random-token prompts of 2048, greedy 16 tokens with the top-5
+    # 32 random-token prompts of 2048, greedy 128 tokens with the top-5
     # log-probabilities: batch 32, its first 8 as batch 8, three requests
-    # alone, and four requests staggered so prefills join running decodes
+    # alone, four requests staggered so prefills join running decodes, and
+    # batch 32 again with its decode steps replayed from a captured graph
     model, prompts = llama3_8b
     b32 = run(model, prompts, MAX_NEW, _all)
     b8 = run(model, prompts[:8], MAX_NEW, _all)
@@ -113,6 +127,10 @@ def test_llama3_8b_shape_batch_1_8_32(llama3_8b):
     mixed = run(model, prompts[8:12], MAX_NEW, _staggered)
     for i in range(4):
         _assert_same(b32[8 + i], mixed[i], f"staggered request {8 + i}")
+    # the bench's serving loop: decode replayed from a captured graph
+    g32 = run_graph(model, prompts, MAX_NEW)
+    for rid in range(BATCH):
+        _assert_same(b32[rid], g32[rid], f"graph request {rid}")
     generated = {tuple(r.tokens[PROMPT_LEN:]) for r in b32.values()}
     assert len(generated) > 1
     assert all(len(r.tokens) == PROMPT_LEN + MAX_NEW for r in b32.values())

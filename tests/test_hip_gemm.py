@@ -133,7 +133,10 @@ def test_gemm_deterministic_across_runs():
 # otherwise. Inputs below keep every K-tile dot exact in fp32, so the result
 # must equal the oracle bit for bit on either path.
 
-_BIG_M = [256, 1024]  # 128 x 128 tiles; 64-bit sums: the 32-bit schedule plus redo from M = 1024
+# 128 x 128 tiles. Unsplit launches with 64-bit sums (fewer than 512
+# K-tiles, f <= 20) run the 32-bit schedule plus the 64-bit redo of marked
+# tiles at every M > 16; split ones the 64-bit kernel.
+_BIG_M = [256, 1024]
 
 
 def _dyadic(shape, lo, hi, exp2, g, dtype):
@@ -219,30 +222,59 @@ def test_gemm_big_split_k_invariance(dtype, M):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_gemm_int64_marked_tile_redo(dtype):
+@pytest.mark.parametrize("M", [1024, 64, 32])
+def test_gemm_int64_marked_tile_redo(dtype, M):
     # unsplit 64-bit sums at M > 16 and f <= 20: 32-bit sums, tiles with a
     # K-tile outside the rounding-constant range marked (NaN at the tile's
-    # first element) and recomputed by the 64-bit kernel. Here some K-tiles'
-    # quantised partials exceed 2^31 (a 32-bit sum would saturate) and a NaN
-    # bias column marks tiles that are in range (a redundant recompute); every
-    # row equals the same row of split M = 512 launches (the 64-bit kernel
-    # throughout) bit for bit, NaN for NaN
-    g = torch.Generator("cpu").manual_seed(77)
-    M, K, N = 1024, 1024, 384
+    # first element) and recomputed by the 64-bit kernel (M = 32 / 64: the
+    # decode-sized rows, unsplit on request). Here some K-tiles' quantised
+    # partials exceed 2^31 (a 32-bit sum would saturate) and a NaN bias
+    # column marks tiles that are in range (a redundant recompute); every row
+    # equals the same row of split launches of half the rows (the 64-bit
+    # kernel throughout) bit for bit, NaN for NaN
+    g = torch.Generator("cpu").manual_seed(77 + M)
+    K, N = 1024, 384
     a = torch.randn(M, K, generator=g).to(dtype)
     b = (torch.randn(K, N, generator=g) * 0.05).to(dtype)
+    r0 = M // 5
     # bf16: |P * 2^16| mostly beyond 2^31; f16 (max 65504): beyond the range check only
-    a[200:210, 128:256] = (a[200:210, 128:256].float() * (1e5 if dtype == torch.bfloat16 else 1e4)).to(dtype)
+    a[r0:r0 + 10, 128:256] = (a[r0:r0 + 10, 128:256].float() * (1e5 if dtype == torch.bfloat16 else 1e4)).to(dtype)
     bias = torch.randn(N, generator=g).to(dtype)
     bias[128] = float("nan")
-    full = _run(a, b, bias, bits=64, frac=16, b_layout="nk")
+    full = _run(a, b, bias, bits=64, frac=16, b_layout="nk", split_k=1)
     assert torch.isnan(full[:, 128]).all() and not torch.isnan(full[:, :128]).any()
-    for m0 in (0, 512):
-        part = _run(a[m0:m0 + 512].contiguous(), b, bias, bits=64, frac=16, b_layout="nk", split_k=2)
-        assert nan_aware_equal(part, full[m0:m0 + 512]), (m0, mismatch_report(part, full[m0:m0 + 512]))
-    want = _oracle(a[195:215], b, bias, 64, 16)
-    report = close_report(full[195:215], want)
+    half = M // 2
+    for m0 in (0, half):
+        part = _run(a[m0:m0 + half].contiguous(), b, bias, bits=64, frac=16, b_layout="nk", split_k=2)
+        assert nan_aware_equal(part, full[m0:m0 + half]), (m0, mismatch_report(part, full[m0:m0 + half]))
+    want = _oracle(a[r0 - 5:r0 + 15], b, bias, 64, 16)
+    report = close_report(full[r0 - 5:r0 + 15], want)
     assert not report, report
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_gemm_decode_shape_kernel_matches_split_path(dtype, M):
+    # 16-bit inputs, M <= 16, N <= 8192, K a multiple of 128, K-contiguous B
+    # (the linear layout): the decode-shape kernel (each workgroup 16 columns
+    # over all of K, its four waves on contiguous K-tile runs, the sums added
+    # through LDS). An explicit split request takes the 16 x 256 tiles split
+    # over K instead. Same bits, equal to the oracle on exact dots, with a
+    # ragged N, a bias and each accumulator width; K-tile counts below, at and
+    # not a multiple of the wave count; every row equals an M = 1 launch of it
+    g = torch.Generator("cpu").manual_seed(31 + M)
+    for K, N in ((128, 1000), (384, 16), (640, 4096), (4096, 8192)):
+        a = _dyadic((M, K), -3, 3, -5, g, dtype)
+        b = _dyadic((K, N), -3, 3, 0, g, dtype)
+        bias = _dyadic((N,), -8, 8, -3, g, dtype)
+        for bits, frac in ((32, 16), (64, 16), (16, 8)):
+            got = _run(a, b, bias, bits=bits, frac=frac, b_layout="nk")
+            split = _run(a, b, bias, bits=bits, frac=frac, b_layout="nk", split_k=2)
+            assert torch.equal(got, split), (K, N, bits, mismatch_report(got, split))
+            want = _oracle(a, b, bias, bits, frac)
+            assert torch.equal(got, want), (K, N, bits, mismatch_report(got, want))
+        row = _run(a[M - 1:].contiguous(), b, bias, b_layout="nk")
+        assert torch.equal(row[0], _run(a, b, bias, b_layout="nk")[M - 1])
 
 
 # --- restated reference tests (fxpr_vllm/_tests/test_gemm.py) ---------------

@@ -9,6 +9,7 @@ identity.
 
 from __future__ import annotations
 
+import ctypes
 import json
 import math
 import pathlib
@@ -18,6 +19,7 @@ import pytest
 import torch
 
 import fxpr_vllm  # noqa: F401
+from fxpr_vllm import _hip
 from fxpr_vllm import config as fxpr_config
 from fxpr_vllm._kernels import rows as K
 from oracle import numerics as N
@@ -404,6 +406,45 @@ def test_log_softmax_split_concurrent_streams():
     torch.cuda.synchronize()
     for i, o in enumerate(outs):
         assert torch.equal(o, want[i % len(xs)]), i
+
+
+def _lsm_fallbacks() -> int:
+    n = ctypes.c_ulonglong(0)
+    _hip.call("fxpr_debug_lsm_fallbacks", ctypes.byref(n))
+    return n.value
+
+
+@pytest.mark.parametrize("max_tries,sum_tries", [(0, None), (None, 0)])
+def test_log_softmax_split_giveup_paths_bit_exact(max_tries, sum_tries):
+    # The split kernel's polls are bounded. The host sets a poll's limit to 0
+    # tries, so every workgroup gives up at once and computes what it waited
+    # for from the input (the row maximum and exact sum, or the exact sum
+    # after its own span sum was published): the bits equal the oracle's and
+    # every kernel exits normally. A normal launch on the same stream right
+    # after must find consistent sync state (its generation advanced by the
+    # last span of each row) and give the same bits again.
+    lib = _hip.load()
+    default = lib.fxpr_debug_lsm_default_spin_limit()
+    rows, cols = 3, 128_256                    # 8 spans of 2004 vectors per row
+    x = _logits(rows, cols, seed=23)
+    x[2, 77_000] = 75.0
+    want = from_np(R.log_softmax(to_np(x), "bf16", "f32", 32, 16), torch.float32)
+    xd = x.to(DEV)
+    torch.cuda.synchronize()
+    before = _lsm_fallbacks()
+    _hip.call("fxpr_debug_set_lsm_spin_limit", default if max_tries is None else max_tries,
+              default if sum_tries is None else sum_tries)
+    try:
+        got = torch.ops.fxpr.log_softmax_fxp(xd, 32, 16, torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        _hip.call("fxpr_debug_set_lsm_spin_limit", default, default)
+    assert _lsm_fallbacks() - before == rows * 8   # every span took the path
+    assert nan_aware_equal(got.cpu(), want), mismatch_report(got.cpu(), want)
+    again = torch.ops.fxpr.log_softmax_fxp(xd, 32, 16, torch.float32)
+    torch.cuda.synchronize()
+    assert _lsm_fallbacks() - before == rows * 8
+    assert torch.equal(again, got)
 
 
 def test_log_softmax_batch_and_run_invariance():

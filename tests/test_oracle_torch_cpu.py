@@ -81,3 +81,30 @@ def test_log_softmax(bits, frac, io_out):
     xs = N.store(x.astype(np.float32), "bf16")
     want = R.log_softmax(xs, "bf16", io_out, bits, frac)
     assert _same(TC.log_softmax(_t(xs), "bf16", io_out, bits, frac), want)
+
+
+@pytest.mark.parametrize("io,b,f", [("bf16", 32, 16), ("f16", 64, 32), ("bf16", 16, 8)])
+def test_decode_attention(io, b, f):
+    # decode rows of several 512-key chunks (distinct chunk maxima), ragged
+    # lengths and a shuffled page table, against the numpy oracle's chunked
+    # algorithm
+    from oracle import attention as OA
+
+    rng = np.random.default_rng(7)
+    R, Hq, Hkv, D, ps = 5, 8, 2, 64, 16
+    sl = np.array([1, 70, 600, 1500, 2049], np.int32)
+    nbk = [-(-int(L) // ps) for L in sl]
+    NB = sum(nbk) + 4
+    perm = rng.permutation(NB)
+    bt = np.zeros((R, max(nbk)), np.int32)
+    off = 0
+    for i, n in enumerate(nbk):
+        bt[i, :n] = perm[off:off + n]
+        off += n
+    kv = rng.standard_normal((NB, 2, ps, Hkv, D)).astype(np.float32) * 2.0
+    q = rng.standard_normal((R, Hq, D)).astype(np.float32)
+    kvs, qs = N.store(kv, io), N.store(q, io)
+    want = OA.unified_attention(qs, kvs, np.arange(R + 1, dtype=np.int32), sl, bt, io, softmax_scale=D ** -0.5,
+                                int_bits=b, frac_bits=f, chunk_keys=OA.CHUNK_KEYS)
+    got = TC.decode_attention(_t(qs), _t(kvs), torch.from_numpy(sl), torch.from_numpy(bt), io, D ** -0.5, b, f)
+    assert _same(got, want)

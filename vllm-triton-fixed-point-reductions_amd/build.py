@@ -40,6 +40,16 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source additions. rows.hip: no atomic optimizer. The split log-softmax
+# counts each workgroup with one returning atomic from one lane, whose return
+# is meant to arrive with the loads issued right after it; the optimizer's
+# lane broadcast would wait for it at once, on every workgroup's critical
+# path.
+FILE_FLAGS = {
+    "rows.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -84,7 +94,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     jobs = jobs or min(8, len(sources))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [
-            ex.submit(_run, [cc, *COMMON_FLAGS, "-c", str(s), "-o", str(o)], verbose)
+            ex.submit(_run, [cc, *COMMON_FLAGS, *FILE_FLAGS.get(s.name, []), "-c", str(s), "-o", str(o)], verbose)
             for s, o in zip(sources, objs)
         ]
         for f in futs:

@@ -1,5 +1,6 @@
 // C-ABI entry points of the paged attention (kernels: attn_impl.h,
 // instantiated per input type in attn_{bf16,f16,f32}.hip).
+#include <algorithm>
 #include <mutex>
 
 #include "attn_impl.h"
@@ -9,7 +10,8 @@ using namespace fxpr::attn;
 
 namespace {
 
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 64;      // automatic policy's largest split count
+constexpr int64_t kMaxGridZ = 65535;  // splits are the launch grid's z dimension
 // Split launches keep per-chunk partials; above this many bytes of them a
 // launch runs unsplit instead (split counts never change the bits).
 constexpr int64_t kSplitWsMax = int64_t(1) << 30;
@@ -47,12 +49,15 @@ WsLayout ws_layout(int64_t num_tokens, int num_heads, int head_dim, int int_bits
 
 }  // namespace
 
-// Split policy. An explicit request wins (each workgroup's key chunks dealt
-// evenly over the splits, as the reference's _split_tile_range deals tiles).
-// Automatic (0), after the reference's _pick_num_splits
-// (attention.py:664-689): no split for short contexts (<= 32 key tiles) or
-// when the (request, kv-head, q-tile) workgroups already oversubscribe the
-// 256 CUs; otherwise splits of a fixed kSplitChunks chunks each, so every
+// Split policy (this build's own; the reference's _pick_num_splits,
+// attention.py:664-689, is the model for its shape). An explicit request wins
+// (each workgroup's key chunks dealt evenly over the splits, as the
+// reference's _split_tile_range deals tiles), up to the number of 512-key
+// chunks a block-table row holds: splits past that would hold no keys (the
+// reference's would be empty), so the launch runs that many. Automatic (0):
+// no split for short contexts (<= 32 key tiles of 64) or when the
+// (request, kv head, 16-row query tile) workgroups already number more than
+// 8 x 256; otherwise one chunk per split (up to 64 splits), so every
 // workgroup carries about the same work whatever its request's length
 // (requests shorter than the longest get empty splits). Split counts never
 // change bits.
@@ -65,8 +70,11 @@ struct SplitPlan {
 
 SplitPlan plan_splits(int num_requests, int num_kv_heads, int group, int max_query_len, int max_blocks,
                       int page_size, int requested) {
-  if (requested >= 1) return {requested > kMaxSplits ? kMaxSplits : requested, 0};
   const int64_t tiles = cdiv(int64_t(max_blocks > 0 ? max_blocks : 1) * page_size, TILE);
+  if (requested >= 1) {
+    const int64_t cap = std::min<int64_t>(std::max<int64_t>(cdiv(tiles, CT), 1), kMaxGridZ);
+    return {int(std::min<int64_t>(requested, cap)), 0};
+  }
   if (tiles <= 32) return {1, 0};
   const int64_t qtiles = cdiv(int64_t(max_query_len > 1 ? max_query_len : 1) * group, QROWS);
   const int64_t base = int64_t(num_requests > 1 ? num_requests : 1) * num_kv_heads * qtiles;
@@ -238,6 +246,10 @@ int static_scratch(hipStream_t st, void** out) {
   if (dev < 0 || dev >= kMaxDevices) return FXPR_E_ARG;
   std::lock_guard<std::mutex> lock(scratch_mu);
   if (scratch_ptr[dev] == nullptr) {
+    // the look-up (and a device switch) stays out of graph capture
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(st, &cs)) != hipSuccess) return static_cast<int>(e);
+    if (cs != hipStreamCaptureStatusNone) return FXPR_E_CAPTURE;
     if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return static_cast<int>(e);
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));

@@ -180,6 +180,8 @@ extern "C" const char* fxpr_error_string(int code) {
     case FXPR_E_SHAPE: return "fxpr: invalid or inconsistent sizes";
     case FXPR_E_WORKSPACE: return "fxpr: workspace missing or too small";
     case FXPR_E_ARG: return "fxpr: invalid argument";
+    case FXPR_E_CAPTURE:
+      return "fxpr: first use on this device while the stream is capturing a graph (make one eager call first)";
     default:
       if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
       return "fxpr: unknown error";

@@ -916,6 +916,133 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
 }
 
 // ---------------------------------------------------------------------------
+// Decode-shape kernel: few rows (MB 16-row fragments), 16-bit inputs,
+// K-contiguous A and B with 16-byte aligned rows and K a multiple of the
+// 128-wide K-tile (the linear layout at decode batch sizes). B streams from
+// HBM once and no split-K partials exist. A workgroup owns 16 columns of C
+// for every row and all of K; its NW waves split the K-tiles into NW
+// contiguous runs of nt = ceil(K-tiles / NW) (the last runs may hold fewer
+// real tiles). A wave loads its fragments straight from global memory into
+// registers in the MFMA operand layout (lane (r, g) of a 16-row x 32-k
+// fragment holds row r, k = 8 g .. 8 g + 7: one 16-byte load; B
+// non-temporal, A re-read through L2), DEPTH K-tiles ahead, and runs the
+// same per-K-tile MFMA chains as every other kernel (16x16x32 in increasing
+// k from a zero accumulator): the bits are theirs. The waves then hand their
+// integer sums to wave 0 through LDS (integers: any order), which adds them
+// and writes C. Every step issues the same loads (a step past the wave's run
+// reads the first 16 bytes of A, never used), so the compiler counts the
+// loads in flight exactly.
+template <int MB_, int NW_, int DEPTH_> struct StreamTile {
+  static constexpr int MB = MB_, NW = NW_, DEPTH = DEPTH_, THREADS = 64 * NW_;
+};
+
+template <int DT, int BITS, class ST>
+__global__ __launch_bounds__(ST::THREADS) void gemm_stream_kernel(GemmArgs args) {
+  using M_ = Mma<DT>;
+  using T = typename M_::T;
+  using AccT = typename Acc<BITS>::T;
+  static_assert(DT != FXPR_DTYPE_F32, "16-bit inputs only");
+  constexpr int MB = ST::MB, NW = ST::NW, D = ST::DEPTH;
+  constexpr int KS = 4;  // 32-k MFMA steps per 128-k K-tile
+  __shared__ AccT red[NW - 1][MB * 4][64];  // waves 1 .. NW - 1 hand their sums to wave 0
+
+  const T* A = static_cast<const T*>(args.a);
+  const T* B = static_cast<const T*>(args.b);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t n0 = int64_t(blockIdx.x) * 16;
+  const int nt = (args.ktiles + NW - 1) / NW;  // steps, every wave
+  const int kt0 = wave * nt;                   // this wave's first K-tile
+  const int r = lane & 15, g = lane >> 4;
+  // rows past M and columns past N are clamped: they feed only outputs that
+  // are never stored
+  const T* bp = B + min<int64_t>(n0 + r, args.N - 1) * args.ldb + g * 8;
+  const T* ap[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) ap[i] = A + min<int64_t>(i * 16 + r, args.M - 1) * args.lda + g * 8;
+
+  struct Frags {
+    uint4 b[KS];
+    uint4 a[MB][KS];
+  };
+  Frags f[D];
+  // step t: K-tile kt0 + t (a stand-in load past the run)
+  auto load = [&](Frags& x, int t) {
+    const bool real = kt0 + t < args.ktiles && t < nt;  // uniform
+    const int64_t k0 = int64_t(kt0 + t) * 128;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      x.b[s] = __builtin_bit_cast(
+          uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(real ? bp + k0 + 32 * s : A)));
+#pragma unroll
+      for (int i = 0; i < MB; ++i) x.a[i][s] = *reinterpret_cast<const uint4*>(real ? ap[i] + k0 + 32 * s : A);
+    }
+  };
+
+  AccT I[MB][4];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) I[i][q] = 0;
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Frags& x) {
+    f32x4 P[MB];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < MB; ++i) P[i] = M_::mma(x.a[i][s], x.b[s], s == 0 ? zero4 : P[i]);
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) I[i][q] = wrap_add<BITS>(I[i][q], quant<BITS>(__fmul_rn(P[i][q], args.scale)));
+  };
+
+  if (nt > 0) {  // uniform (K > 0)
+    static_for<D - 1>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      load(f[j], j);
+    });
+    for (int t = 0; t < nt; t += D) {
+      static_for<D>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        load(f[(j + D - 1) % D], t + j + D - 1);
+        if (t + j < nt && kt0 + t + j < args.ktiles) compute(f[j]);  // uniform
+      });
+    }
+  }
+
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wave - 1][i * 4 + q][lane] = I[i][q];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < NW - 1; ++w)
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) I[i][q] = wrap_add<BITS>(I[i][q], red[w][i * 4 + q][lane]);
+  // lane (r, g) holds rows 16 i + 4 g + q of column n0 + r
+  const int64_t n = n0 + r;
+  if (n >= args.N) return;
+  const float bv = args.bias ? args.bias[n] : 0.0f;
+  T* C = static_cast<T*>(args.c);
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t m = i * 16 + 4 * g + q;
+      if (m >= args.M) continue;
+      float v = acc_to_f32<BITS>(I[i][q], args.inv_scale);
+      if (args.bias) v = __fadd_rn(v, bv);
+      C[m * args.scm + n * args.scn] = Io<DT>::store(v);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 
 template <int DT, class TL> constexpr size_t lds_bytes() {
@@ -970,6 +1097,32 @@ int launch_cfg(GemmArgs a, int splits, hipStream_t st) {
   return launch_tile<DT, BITS, TL, BNC, VEC, false>(a, splits, st);
 }
 
+// Decode-shape kernel launch: one 16-row fragment (M <= 16), four waves,
+// four K-tiles in flight per wave. It is taken where it beats split-K on the
+// large tiles (graph-timed, bf16, K = 4096 / 14336): M <= 16 with N <= 8192,
+// e.g. N = 4096 at M = 1: 10 against 17 us; N = 6144: 15 against 18 us;
+// K = 14336: 28 against 34 us. Wider N streams as fast or faster from the
+// long-lived 16 x 256 tiles (N = 28672 / 128256 at M = 1: 43 / 170 us; a
+// persistent form of this kernel took 44 / 185), and M = 32 / 64 from the
+// 128 x 128 tiles split over K (N = 4096: 20 / 23 us; 32- / 64-row fragments
+// here took 16 / 50).
+constexpr int64_t kStreamMaxM = 16, kStreamMaxN = 8192;
+
+// Shapes the decode-shape kernel takes (16-bit inputs, unsplit)
+inline bool stream_shape(int64_t M, int64_t N) { return M <= kStreamMaxM && N <= kStreamMaxN; }
+inline bool stream_ok(const GemmArgs& a, bool vec, bool b_ncontig) {
+  return vec && !b_ncontig && stream_shape(a.M, a.N) && a.K % 128 == 0;
+}
+
+template <int DT, int BITS, class ST> int launch_stream_tile(const GemmArgs& a, hipStream_t st) {
+  gemm_stream_kernel<DT, BITS, ST><<<dim3(unsigned(cdiv(a.N, 16))), ST::THREADS, 0, st>>>(a);
+  return launch_status();
+}
+
+template <int DT, int BITS> int launch_stream(const GemmArgs& a, hipStream_t st) {
+  return launch_stream_tile<DT, BITS, StreamTile<1, 4, 4>>(a, st);
+}
+
 // Tile configuration by M. Only speed depends on it: every config issues the
 // same MFMA chain per output element.
 enum class TileId { M16, M32, M64, Big };
@@ -1010,6 +1163,10 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
   // faster (153 against 176 us).
   const bool big_ok = vec && !b_ncontig && big_rows(a.M) && a.lda <= (int64_t(1) << 22) &&
                       a.ldb <= (int64_t(1) << 22);
+  if constexpr (DT != FXPR_DTYPE_F32) {
+    // decode shapes: stream B once, no split-K partials
+    if (splits <= 1 && stream_ok(a, vec, b_ncontig)) return launch_stream<DT, BITS>(a, st);
+  }
   if constexpr (DT != FXPR_DTYPE_F32 && BITS == 64) {
     if (big_ok) {
       // Unsplit, fewer than 512 K-tiles: 32-bit sums in the two-workgroups-
@@ -1058,8 +1215,10 @@ int run_gemm(GemmArgs a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
 
 inline int ktile_for(int io_dtype) { return io_dtype == FXPR_DTYPE_F32 ? 64 : 128; }
 
-// Split count: explicit request wins (clamped to the K-tile count); otherwise
-// split only when the output tiles cannot fill the 256 CUs about twice.
+// Split count: explicit request wins (clamped to the K-tile count);
+// otherwise none for the shapes of the decode-shape kernel (16-bit, M <= 16,
+// N <= 8192), and elsewhere a split only when the output tiles cannot fill
+// the 256 CUs about twice: 512 / tiles splits, at most 16.
 inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int requested) {
   const int ktiles = int(cdiv(K, ktile_for(io_dtype)));
   if (ktiles <= 1) return 1;
@@ -1067,6 +1226,8 @@ inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int req
   if (requested >= 1) {
     s = requested;
   } else {
+    // 16-bit decode shapes take the streaming kernel, which needs no split
+    if (io_dtype != FXPR_DTYPE_F32 && stream_shape(M, N)) return 1;
     int bm, bn;
     tile_dims(pick_tile(M), bm, bn);
     if (big_rows(M) && io_dtype != FXPR_DTYPE_F32) {

@@ -362,23 +362,34 @@ __global__ __launch_bounds__(kLsmThreads) void log_softmax_kernel(
 // than the previous launch's. Wave 0 of every workgroup polls the row's words
 // (one lane per word, agent-scope atomic loads) until all carry the tag. A
 // word is written and read whole, so no ordering between different words is
-// needed, hence no fences. The generation is read at the start by every
-// workgroup of the row and advanced by span 0 once every span's sum is there
-// (every span has read it by then).
+// needed, hence no fences.
 // The host takes this kernel only when the whole grid fits on the GPU at once,
-// so no poll waits for a workgroup that cannot start; the poll is bounded
-// nonetheless (about a second), and a row whose wait gave up is written as
-// NaN.
+// so normally no poll waits for a workgroup that cannot start. Work of other
+// kernels or processes on the CUs can still hold a row's spans back, so the
+// poll is bounded (about 2^14 tries of an L2 round trip, milliseconds): a
+// workgroup whose poll gives up reads the whole row from HBM and computes
+// the row maximum and the exact row sum itself (the same integers, so the
+// same bits), still publishing its own words for its siblings.
+// Every span reads the generation at its start and counts itself in the
+// row's start count later (an atomic add issued with its sum word, whose
+// return arrives with the sums poll's first loads); the span that completes
+// the count resets it and advances the generation. So the generation moves
+// only after every span of the launch has read it: a span that starts late,
+// after its siblings gave up waiting and finished, still takes its launch's
+// tag, and no word of one launch can carry the next launch's tag. Launches on
+// one stream do not overlap, so the next launch finds the count at zero and
+// the new generation.
 
 constexpr int kSplitMax = 16;        // workgroups per row, a power of two
 constexpr int kSplitRows = 1024;     // rows of one split launch
 constexpr int kSplitThreads = 256;
 constexpr int kSplitNreg = 8;        // 16-byte vectors per thread
 constexpr int kSplitMinVectors = 4096;  // shorter rows take the one-workgroup kernel
-constexpr int kSpinLimit = 1 << 20;
+constexpr int kSpinLimit = 1 << 14;
 
 struct LsmSync {
   uint32_t generation[kSplitRows];
+  uint32_t started[kSplitRows];               // spans of the running launch that have read the generation
   uint64_t maxima[kSplitRows][kSplitMax];     // tag | fp32 bit pattern
   uint64_t sums[kSplitRows][kSplitMax * 4];   // tag | 32 bits of a span sum, low word first
 };
@@ -397,13 +408,17 @@ template <class U> __device__ __forceinline__ U load_agent(U* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wave 0: lane i < n polls words[i] until all n carry the tag; the lane's
-// 32-bit value in *val. False if the bounded poll gave up.
-__device__ __forceinline__ bool poll_tagged(uint64_t* words, int n, uint32_t tag, uint32_t* val) {
+// Split launches whose poll gave up at least once per span (read by
+// fxpr_debug_lsm_fallbacks; the kernels only add to it).
+__device__ unsigned long long lsm_fallbacks;
+
+// Wave 0: lane i < n polls words[i] until all n carry the tag, at most
+// `tries` times; the lane's 32-bit value in *val. False if the poll gave up.
+__device__ __forceinline__ bool poll_tagged(uint64_t* words, int n, uint32_t tag, uint32_t* val, int tries) {
   const int lane = threadIdx.x & 63;
   uint64_t w = 0;
   bool ok = false;
-  for (int it = 0; it < kSpinLimit; ++it) {
+  for (int it = 0; it < tries; ++it) {
     if (lane < n) w = load_agent(words + lane);
     if (__builtin_amdgcn_ballot_w64(lane < n && uint32_t(w >> 32) != tag) == 0) {
       ok = true;
@@ -415,19 +430,84 @@ __device__ __forceinline__ bool poll_tagged(uint64_t* words, int n, uint32_t tag
   return ok;
 }
 
+// Thread 0, at the end of its span: the span that completed the row's start
+// count (`before`, the count it found, is split - 1) resets it and advances
+// the generation to the launch's tag.
+__device__ __forceinline__ void lsm_advance(LsmSync* sync, int row, int split, uint32_t tag, uint32_t before) {
+  if (before == uint32_t(split - 1)) {
+    store_agent(&sync->started[row], 0u);
+    store_agent(&sync->generation[row], tag);
+  }
+}
+
+// A span whose poll gave up (workgroup-uniform). It reads the whole row back
+// from the input and computes the row's maximum (if that exchange was lost)
+// and exact sum itself, publishes its own span sum if it had not yet (late
+// siblings may wait for it), writes its span's outputs from the input, and
+// arrives. The span's registers are not used: this path never rejoins the
+// common one, which keeps its 64 VGPRs without spills.
+template <int XDT, int YDT, int VEC, int BITS, int NW>
+__device__ __forceinline__ void lsm_span_fallback(
+    const Vec<typename Io<XDT>::T, VEC>* xrow, Vec<typename Io<YDT>::T, VEC>* yrow, int64_t nchunks, int64_t lo,
+    int n, bool need_max, float m, int frac, float inv_scale, float* fred, uint64_t* ired, LsmSync* sync,
+    int row, int part, int split, uint32_t tag, uint32_t before) {
+  using XV = Vec<typename Io<XDT>::T, VEC>;
+  using YV = Vec<typename Io<YDT>::T, VEC>;
+  const int tid = threadIdx.x;
+  if (need_max) {
+    float mr = -__builtin_inff();
+    for (int64_t c = tid; c < nchunks; c += kSplitThreads) {
+      const XV xv = xrow[c];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) mr = __builtin_elementwise_maximum(mr, Io<XDT>::load(xv.v[j]));
+    }
+    m = block_max(mr, fred);
+  }
+  uint64_t total = 0, mine = 0;
+  for (int64_t c = tid; c < nchunks; c += kSplitThreads) {
+    uint64_t t = 0;
+    add_terms_exact<XDT, VEC, BITS>(xrow[c], m, frac, t);
+    total += t;
+    if (c >= lo && c < lo + n) mine += t;
+  }
+  total = block_exact_sum(total, ired);
+  if (need_max) {
+    mine = block_exact_sum(mine, ired);
+    if (tid < NW)
+      store_agent(&sync->sums[row][part * NW + tid], (uint64_t(tag) << 32) | uint32_t(mine >> (32 * tid)));
+  }
+  const float lse = lse_of(m, total, inv_scale);
+  for (int c = tid; c < n; c += kSplitThreads) {
+    const XV xv = xrow[lo + c];
+    YV yv;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) yv.v[j] = Io<YDT>::store(__fsub_rn(Io<XDT>::load(xv.v[j]), lse));
+    yrow[lo + c] = yv;
+  }
+  if (tid == 0) {
+    __hip_atomic_fetch_add(&lsm_fallbacks, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (need_max)  // gave up before the sums: not counted yet
+      before = __hip_atomic_fetch_add(&sync->started[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lsm_advance(sync, row, split, tag, before);
+  }
+}
+
 // Eight waves per SIMD (at most 64 VGPRs): eight workgroups per CU.
 template <int XDT, int YDT, int VEC, int BITS, bool WIDE>
 __global__ __launch_bounds__(kSplitThreads, 8) void log_softmax_split_kernel(
     const typename Io<XDT>::T* __restrict__ x, typename Io<YDT>::T* __restrict__ y, int64_t cols,
-    int frac, float inv_scale, int fast_sum, int split_log2, LsmSync* __restrict__ sync) {
+    int frac, float inv_scale, int fast_sum, int split_log2, LsmSync* __restrict__ sync, int max_tries,
+    int sum_tries) {
+  static_assert(!WIDE, "span sums are exchanged as 64-bit values");
   using XV = Vec<typename Io<XDT>::T, VEC>;
   using YV = Vec<typename Io<YDT>::T, VEC>;
   using SumT = LseSum<WIDE>;
   constexpr int NREG = kSplitNreg;
-  constexpr int NW = WIDE ? 4 : 2;  // 32-bit words of a span sum
+  constexpr int NW = 2;  // 32-bit words of a span sum
   __shared__ float fred[kSplitThreads / 64];
   __shared__ SumT ired[kSplitThreads / 64];
   __shared__ float row_max, row_lse_value;
+  __shared__ int lost;  // a poll gave up
 
   const int split = 1 << split_log2;
   const int row = static_cast<int>(blockIdx.x >> split_log2);
@@ -438,19 +518,24 @@ __global__ __launch_bounds__(kSplitThreads, 8) void log_softmax_split_kernel(
   const int n = static_cast<int>(max<int64_t>(min<int64_t>(lo + per, nchunks) - lo, 0));
   const int tid = threadIdx.x;
   const bool wave0 = tid < 64;
-  const XV* xr = reinterpret_cast<const XV*>(x + int64_t(row) * cols) + lo;
-  YV* yr = reinterpret_cast<YV*>(y + int64_t(row) * cols) + lo;
+  const XV* xrow = reinterpret_cast<const XV*>(x + int64_t(row) * cols);
+  YV* yrow = reinterpret_cast<YV*>(y + int64_t(row) * cols);
+  const XV* xr = xrow + lo;
+  YV* yr = yrow + lo;
 
-  // the row's tag (wave 0 only), read alongside the span
-  uint32_t tag = 0;
-  if (wave0) tag = load_agent(&sync->generation[row]) + 1;
+  // the row's tag, read alongside the span (by every thread: one cache line,
+  // and no branch whose join would wait for the load before the span's)
+  const uint32_t tag = load_agent(&sync->generation[row]) + 1;
   XV keep[NREG];
-  float m = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < NREG; ++i) {
     const int c = tid + i * kSplitThreads;
-    if (c < n) {
-      keep[i] = nt_load(xr + c);
+    if (c < n) keep[i] = nt_load(xr + c);
+  }
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < NREG; ++i) {
+    if (tid + i * kSplitThreads < n) {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) m = __builtin_elementwise_maximum(m, Io<XDT>::load(keep[i].v[j]));
     }
@@ -459,13 +544,21 @@ __global__ __launch_bounds__(kSplitThreads, 8) void log_softmax_split_kernel(
   if (wave0) {
     if (tid == 0) store_agent(&sync->maxima[row][part], (uint64_t(tag) << 32) | __float_as_uint(m));
     uint32_t v;
-    const bool ok = poll_tagged(sync->maxima[row], split, tag, &v);
+    const bool ok = poll_tagged(sync->maxima[row], split, tag, &v, max_tries);
     float mm = tid < split ? __uint_as_float(v) : -__builtin_inff();
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) mm = __builtin_elementwise_maximum(mm, __shfl_xor(mm, o, 64));
-    if (tid == 0) row_max = ok ? mm : __builtin_nanf("");
+    if (tid == 0) {
+      row_max = mm;
+      lost = ok ? 0 : 1;
+    }
   }
   __syncthreads();
+  if (lost != 0) {  // workgroup-uniform; the siblings are late: no sum exchange either
+    lsm_span_fallback<XDT, YDT, VEC, BITS, NW>(xrow, yrow, nchunks, lo, n, true, 0.f, frac, inv_scale, fred, ired,
+                                              sync, row, part, split, tag, 0u);
+    return;
+  }
   m = row_max;
 
   SumT acc = 0;
@@ -486,23 +579,31 @@ __global__ __launch_bounds__(kSplitThreads, 8) void log_softmax_split_kernel(
     for (int i = 0; i < NREG; ++i) asm volatile("" : "+v"(keep[i].v));
   }
   const SumT span_sum = block_exact_sum(acc, ired);
+  uint32_t before = 0;
   if (wave0) {
     if (tid < NW)
       store_agent(&sync->sums[row][part * NW + tid], (uint64_t(tag) << 32) | uint32_t(span_sum >> (32 * tid)));
+    // count this span in the row's start count (it read the generation long
+    // ago); the atomic's return comes with the poll's first loads
+    if (tid == 0)
+      before = __hip_atomic_fetch_add(&sync->started[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t v;
-    const bool ok = poll_tagged(sync->sums[row], split * NW, tag, &v);
+    const bool ok = poll_tagged(sync->sums[row], split * NW, tag, &v, sum_tries);
     SumT total = tid < split * NW ? static_cast<SumT>(v) << (32 * (tid % NW)) : 0;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      if constexpr (WIDE) total += shfl_xor_u128(total, o);
-      else total += __shfl_xor(total, o, 64);
-    }
+    for (int o = 1; o < 64; o <<= 1) total += __shfl_xor(total, o, 64);
     if (tid == 0) {
-      row_lse_value = ok ? lse_of(m, total, inv_scale) : __builtin_nanf("");
-      if (part == 0) store_agent(&sync->generation[row], tag);
+      row_lse_value = lse_of(m, total, inv_scale);
+      lost = ok ? 0 : 1;
+      if (ok) lsm_advance(sync, row, split, tag, before);
     }
   }
   __syncthreads();
+  if (lost != 0) {  // workgroup-uniform: the row sum from the input (own sum already published)
+    lsm_span_fallback<XDT, YDT, VEC, BITS, NW>(xrow, yrow, nchunks, lo, n, false, m, frac, inv_scale, fred, ired,
+                                              sync, row, part, split, tag, before);
+    return;
+  }
   const float lse = row_lse_value;
 #pragma unroll
   for (int i = 0; i < NREG; ++i) {
@@ -524,6 +625,10 @@ int stream_device(hipStream_t st, int* dev) {
   if (e != hipSuccess) return static_cast<int>(e);
   return (*dev < 0 || *dev >= kMaxDevices) ? FXPR_E_ARG : FXPR_OK;
 }
+
+// Poll tries of the split kernel for the maxima and for the sums
+// (fxpr_debug_set_lsm_spin_limit lowers them to exercise the give-up paths).
+std::atomic<int> lsm_max_tries{kSpinLimit}, lsm_sum_tries{kSpinLimit};
 
 std::mutex sync_mu;
 struct DeviceSync {
@@ -591,7 +696,8 @@ bool try_lsm_split(const void* x, void* y, int64_t rows, int64_t cols, int frac,
   const int fast = BITS != 64 && lse_fast_sum(BITS, frac, double(kSplitNreg) * VEC);
   kernel<<<dim3(static_cast<unsigned>(rows << lg)), kSplitThreads, 0, st>>>(
       static_cast<const typename Io<XDT>::T*>(x), static_cast<typename Io<YDT>::T*>(y), cols, frac,
-      pow2f(-frac), fast, lg, sync);
+      pow2f(-frac), fast, lg, sync, lsm_max_tries.load(std::memory_order_relaxed),
+      lsm_sum_tries.load(std::memory_order_relaxed));
   *rc = launch_status();
   return true;
 }
@@ -692,4 +798,20 @@ extern "C" int fxpr_log_softmax(const void* x, int x_dtype, void* y, int y_dtype
       return launch_lsm<FXPR_DTYPE_F32, FXPR_DTYPE_F32>(x, y, rows, cols, int_bits, frac_bits, st);
     default: return FXPR_E_DTYPE;
   }
+}
+
+extern "C" int fxpr_debug_set_lsm_spin_limit(int max_tries, int sum_tries) {
+  if (max_tries < 0 || sum_tries < 0) return FXPR_E_ARG;
+  lsm_max_tries.store(max_tries, std::memory_order_relaxed);
+  lsm_sum_tries.store(sum_tries, std::memory_order_relaxed);
+  return FXPR_OK;
+}
+
+extern "C" int fxpr_debug_lsm_default_spin_limit(void) { return kSpinLimit; }
+
+extern "C" int fxpr_debug_lsm_fallbacks(unsigned long long* count) {
+  if (!count) return FXPR_E_ARG;
+  const hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(lsm_fallbacks), sizeof(*count), 0,
+                                           hipMemcpyDeviceToHost);
+  return e == hipSuccess ? FXPR_OK : static_cast<int>(e);
 }

@@ -48,6 +48,10 @@ SIGNATURES: dict[str, list] = {
     "fxpr_attention_splits": [_I, _I, _I, _I, _I, _I, _I],
     "fxpr_reshape_and_cache": [_P, _P, _P, _P, _I, _P, _L, _I, _I, _I, _L,
                                _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P],
+    # test hooks of the split log-softmax's bounded polls
+    "fxpr_debug_set_lsm_spin_limit": [_I, _I],
+    "fxpr_debug_lsm_default_spin_limit": [],
+    "fxpr_debug_lsm_fallbacks": [ctypes.POINTER(ctypes.c_ulonglong)],
 }
 
 # entry points that return something other than an int status
