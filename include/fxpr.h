@@ -118,6 +118,31 @@ int fxpr_log_softmax(const void* x, int x_dtype, void* y, int y_dtype,
                      void* stream);
 
 /*
+ * Vocab-parallel log-softmax (rows whose columns are split over devices, as
+ * a vocab-parallel lm_head leaves its logits). Per shard [rows, cols]:
+ * fxpr_log_softmax_shard_max writes each row's maximum (fp32, NaN if any
+ * element is NaN); the shards' maxima are combined by a MAX. Then
+ * fxpr_log_softmax_shard_sum writes each row's exact integer sum (int64) of
+ * float_to_fixed(exp(x - m), int_bits, frac_bits) against the combined
+ * maximum m, the same terms fxpr_log_softmax sums; the shards' sums are
+ * combined by an integer SUM (any order). fxpr_log_softmax_shard_finish then
+ * writes the shard's outputs, y = OUT(x - (m + log(fl32(S) * 2^-frac_bits))).
+ * The outputs equal fxpr_log_softmax's on the whole rows bit for bit while a
+ * row's total stays below 2^63 (frac_bits <= 32, cols < 2^29 per shard).
+ * No counterpart in the reference (its log-softmax is not shipped; README.md:60).
+ */
+int fxpr_log_softmax_shard_max(const void* x, int x_dtype, float* row_max,
+                               int64_t rows, int64_t cols, void* stream);
+int fxpr_log_softmax_shard_sum(const void* x, int x_dtype,
+                               const float* row_max, int64_t* row_sum,
+                               int64_t rows, int64_t cols, int int_bits,
+                               int frac_bits, void* stream);
+int fxpr_log_softmax_shard_finish(const void* x, int x_dtype,
+                                  const float* row_max, const int64_t* row_sum,
+                                  void* y, int y_dtype, int64_t rows,
+                                  int64_t cols, int frac_bits, void* stream);
+
+/*
  * Test hooks of fxpr_log_softmax's split-row kernel (no counterpart in the
  * reference). The kernel's workgroups of one row exchange their span maxima,
  * then their exact span sums, through device memory, polling each exchange
@@ -173,6 +198,28 @@ int fxpr_gemm(const void* a, const void* b, const float* bias, void* c,
               int64_t stride_bn, int64_t stride_cm, int64_t stride_cn,
               int int_bits, int frac_bits, int split_k, void* workspace,
               int64_t workspace_bytes, void* stream);
+
+/*
+ * Row-parallel (K-sharded) GEMM. fxpr_gemm_partial writes the integer
+ * accumulators acc[m][n] (row-major [m, n]; int32 for int_bits 16 and 32,
+ * int64 for 64) = wrapping sum over this call's K-tiles of
+ * RNE_sat_b(P_t[m, n] * 2^frac_bits), the sums fxpr_gemm converts. A
+ * K-shard's accumulators add up (integer SUM across shards, any order) to
+ * the unsharded ones when its first column is a K-tile boundary of the full
+ * K (a multiple of 128 for 16-bit inputs, 64 for fp32). fxpr_gemm_finish
+ * applies fxpr_gemm's epilogue to summed accumulators (wrapped to int_bits):
+ * C = IO(fl32(acc) * 2^-frac_bits (+ bias)), bias fp32 or NULL. Together they
+ * give fxpr_gemm's bits. No counterpart in the reference, whose row-parallel
+ * linears all-reduce bf16 outputs (quantisation_config.py:80-96).
+ */
+int fxpr_gemm_partial(const void* a, const void* b, void* acc, int io_dtype,
+                      int64_t m, int64_t n, int64_t k, int64_t stride_am,
+                      int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                      int int_bits, int frac_bits, void* stream);
+int fxpr_gemm_finish(const void* acc, const float* bias, void* c,
+                     int io_dtype, int64_t m, int64_t n, int64_t stride_cm,
+                     int64_t stride_cn, int int_bits, int frac_bits,
+                     void* stream);
 
 /* Split count fxpr_gemm will use for this shape and request.
  * Host-side policy of the reference: _resolve_split_k (gemm.py:385-412). */

@@ -88,7 +88,13 @@ struct GemmArgs {
   // gemm_big_kernel: compute only the output tiles whose first element C[m0][n0]
   // is NaN (the marks of the int32-accumulating pass of a 64-bit launch)
   int redo_marked;
+  // kPartial: write the integer accumulators to ws ([M][N], the split-K
+  // layout with one split) instead of C; kFinish: only the epilogue, from the
+  // accumulators in ws to C
+  int mode;
 };
+
+enum GemmMode { kFull = 0, kPartial = 1, kFinish = 2 };
 
 template <int BITS> struct Acc { using T = int32_t; };
 template <> struct Acc<64> { using T = int64_t; };
@@ -1084,7 +1090,7 @@ int launch_big(GemmArgs a, int splits, hipStream_t st) {
   if constexpr (WIDEN) {
     return go(gemm_big_kernel<DT, BITS, BT, false, true>);
   } else {
-    if (splits > 1) return go(gemm_big_kernel<DT, BITS, BT, true>);
+    if (splits > 1 || a.mode == kPartial) return go(gemm_big_kernel<DT, BITS, BT, true>);
     return go(gemm_big_kernel<DT, BITS, BT, false>);
   }
 }
@@ -1093,7 +1099,7 @@ template <int DT, int BITS, class TL, bool BNC, bool VEC>
 int launch_cfg(GemmArgs a, int splits, hipStream_t st) {
   a.tiles_m = int(cdiv(a.M, TL::BM));
   a.tiles_n = int(cdiv(a.N, TL::BN));
-  if (splits > 1) return launch_tile<DT, BITS, TL, BNC, VEC, true>(a, splits, st);
+  if (splits > 1 || a.mode == kPartial) return launch_tile<DT, BITS, TL, BNC, VEC, true>(a, splits, st);
   return launch_tile<DT, BITS, TL, BNC, VEC, false>(a, splits, st);
 }
 
@@ -1163,9 +1169,10 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
   // faster (153 against 176 us).
   const bool big_ok = vec && !b_ncontig && big_rows(a.M) && a.lda <= (int64_t(1) << 22) &&
                       a.ldb <= (int64_t(1) << 22);
+  const bool full = a.mode == kFull;
   if constexpr (DT != FXPR_DTYPE_F32) {
     // decode shapes: stream B once, no split-K partials
-    if (splits <= 1 && stream_ok(a, vec, b_ncontig)) return launch_stream<DT, BITS>(a, st);
+    if (full && splits <= 1 && stream_ok(a, vec, b_ncontig)) return launch_stream<DT, BITS>(a, st);
   }
   if constexpr (DT != FXPR_DTYPE_F32 && BITS == 64) {
     if (big_ok) {
@@ -1175,7 +1182,7 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
       // K-tile outside the rounding-constant range). Only for f <= 20 (|P| < 4
       // per K-tile stays in range; at larger f most tiles would be computed
       // twice). 1.4-1.8x faster than the exact kernel alone from M = 65 up.
-      if (splits <= 1 && a.ktiles < 512 && a.fast_lim >= 4.0f) {
+      if (full && splits <= 1 && a.ktiles < 512 && a.fast_lim >= 4.0f) {
         const int rc = launch_big<DT, 32, TB2, true>(a, 1, st);
         if (rc != FXPR_OK) return rc;
         GemmArgs b = a;
@@ -1206,8 +1213,10 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
 
 template <int DT, int BITS>
 int run_gemm(GemmArgs a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
-  int rc = dispatch_tile<DT, BITS>(a, b_ncontig, vec, splits, st);
-  if (rc != FXPR_OK || splits <= 1) return rc;
+  if (a.mode != kFinish) {
+    const int rc = dispatch_tile<DT, BITS>(a, b_ncontig, vec, splits, st);
+    if (rc != FXPR_OK || splits <= 1 || a.mode == kPartial) return rc;
+  }
   const int64_t mn = a.M * a.N;
   gemm_splitk_reduce_kernel<DT, BITS><<<dim3(unsigned(cdiv(mn, 256))), 256, 0, st>>>(a, splits);
   return launch_status();

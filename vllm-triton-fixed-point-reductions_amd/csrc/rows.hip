@@ -744,6 +744,112 @@ int launch_lsm(const void* x, void* y, int64_t rows, int64_t cols, int bits, int
   return launch_lsm_vec<XDT, YDT, 1>(x, y, rows, cols, bits, frac, st);
 }
 
+// ---------------------------------------------------------------------------
+// Vocab-parallel log-softmax: rows whose columns are split over devices (a
+// vocab-parallel lm_head's logits). Each shard's row maxima, combined by a
+// MAX across shards; each shard's exact integer row sums of the same terms as
+// the whole-row kernels, against the combined maxima, combined by an integer
+// SUM (order-free); then each shard's outputs from the combined maximum and
+// sum. The bits equal fxpr_log_softmax on the whole rows while a row's total
+// stays below 2^63 (f <= 32 and rows below 2^29 columns).
+
+constexpr int kShardThreads = 256;
+
+template <int XDT, int VEC>
+__global__ __launch_bounds__(kShardThreads) void lsm_shard_max_kernel(const typename Io<XDT>::T* __restrict__ x,
+                                                                      float* __restrict__ out, int64_t cols) {
+  using XV = Vec<typename Io<XDT>::T, VEC>;
+  __shared__ float fred[kShardThreads / 64];
+  const XV* xr = reinterpret_cast<const XV*>(x + int64_t(blockIdx.x) * cols);
+  float m = -__builtin_inff();
+  for (int64_t c = threadIdx.x; c < cols / VEC; c += kShardThreads) {
+    const XV xv = xr[c];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) m = __builtin_elementwise_maximum(m, Io<XDT>::load(xv.v[j]));
+  }
+  m = block_max(m, fred);
+  if (threadIdx.x == 0) out[blockIdx.x] = m;
+}
+
+template <int XDT, int VEC, int BITS>
+__global__ __launch_bounds__(kShardThreads) void lsm_shard_sum_kernel(const typename Io<XDT>::T* __restrict__ x,
+                                                                      const float* __restrict__ row_max,
+                                                                      int64_t* __restrict__ out, int64_t cols,
+                                                                      int frac) {
+  using XV = Vec<typename Io<XDT>::T, VEC>;
+  __shared__ uint64_t ired[kShardThreads / 64];
+  const XV* xr = reinterpret_cast<const XV*>(x + int64_t(blockIdx.x) * cols);
+  const float m = row_max[blockIdx.x];
+  uint64_t acc = 0;
+  for (int64_t c = threadIdx.x; c < cols / VEC; c += kShardThreads) add_terms_exact<XDT, VEC, BITS>(xr[c], m, frac, acc);
+  acc = block_exact_sum(acc, ired);
+  if (threadIdx.x == 0) out[blockIdx.x] = static_cast<int64_t>(acc);
+}
+
+template <int XDT, int YDT, int VEC>
+__global__ __launch_bounds__(kShardThreads) void lsm_shard_finish_kernel(
+    const typename Io<XDT>::T* __restrict__ x, const float* __restrict__ row_max,
+    const int64_t* __restrict__ row_sum, typename Io<YDT>::T* __restrict__ y, int64_t cols, float inv_scale) {
+  using XV = Vec<typename Io<XDT>::T, VEC>;
+  using YV = Vec<typename Io<YDT>::T, VEC>;
+  const XV* xr = reinterpret_cast<const XV*>(x + int64_t(blockIdx.x) * cols);
+  YV* yr = reinterpret_cast<YV*>(y + int64_t(blockIdx.x) * cols);
+  const float lse = lse_of(row_max[blockIdx.x], static_cast<uint64_t>(row_sum[blockIdx.x]), inv_scale);
+  for (int64_t c = threadIdx.x; c < cols / VEC; c += kShardThreads) {
+    const XV xv = xr[c];
+    YV yv;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) yv.v[j] = Io<YDT>::store(__fsub_rn(Io<XDT>::load(xv.v[j]), lse));
+    yr[c] = yv;
+  }
+}
+
+// 16-byte vectors when the rows allow them, else element by element.
+template <int XDT> bool shard_vec(const void* x, int64_t cols, const void* y = nullptr, int y_bytes = 0) {
+  constexpr int VEC = 16 / sizeof(typename Io<XDT>::T);
+  return cols % VEC == 0 && aligned(x, 16) && (y == nullptr || aligned(y, uintptr_t(y_bytes) * VEC));
+}
+
+template <int XDT> int launch_shard_max(const void* x, float* out, int64_t rows, int64_t cols, hipStream_t st) {
+  using T = typename Io<XDT>::T;
+  constexpr int VEC = 16 / sizeof(T);
+  if (shard_vec<XDT>(x, cols))
+    lsm_shard_max_kernel<XDT, VEC><<<unsigned(rows), kShardThreads, 0, st>>>(static_cast<const T*>(x), out, cols);
+  else
+    lsm_shard_max_kernel<XDT, 1><<<unsigned(rows), kShardThreads, 0, st>>>(static_cast<const T*>(x), out, cols);
+  return launch_status();
+}
+
+template <int XDT, int BITS>
+int launch_shard_sum(const void* x, const float* m, int64_t* out, int64_t rows, int64_t cols, int frac,
+                     hipStream_t st) {
+  using T = typename Io<XDT>::T;
+  constexpr int VEC = 16 / sizeof(T);
+  if (shard_vec<XDT>(x, cols))
+    lsm_shard_sum_kernel<XDT, VEC, BITS><<<unsigned(rows), kShardThreads, 0, st>>>(static_cast<const T*>(x), m,
+                                                                                    out, cols, frac);
+  else
+    lsm_shard_sum_kernel<XDT, 1, BITS><<<unsigned(rows), kShardThreads, 0, st>>>(static_cast<const T*>(x), m, out,
+                                                                                  cols, frac);
+  return launch_status();
+}
+
+template <int XDT, int YDT>
+int launch_shard_finish(const void* x, const float* m, const int64_t* s, void* y, int64_t rows, int64_t cols,
+                        int frac, hipStream_t st) {
+  using XT = typename Io<XDT>::T;
+  using YT = typename Io<YDT>::T;
+  constexpr int VEC = 16 / sizeof(XT);
+  const float inv = pow2f(-frac);
+  if (shard_vec<XDT>(x, cols, y, sizeof(YT)))
+    lsm_shard_finish_kernel<XDT, YDT, VEC><<<unsigned(rows), kShardThreads, 0, st>>>(
+        static_cast<const XT*>(x), m, s, static_cast<YT*>(y), cols, inv);
+  else
+    lsm_shard_finish_kernel<XDT, YDT, 1><<<unsigned(rows), kShardThreads, 0, st>>>(
+        static_cast<const XT*>(x), m, s, static_cast<YT*>(y), cols, inv);
+  return launch_status();
+}
+
 }  // namespace
 }  // namespace fxpr
 
@@ -814,4 +920,67 @@ extern "C" int fxpr_debug_lsm_fallbacks(unsigned long long* count) {
   const hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(lsm_fallbacks), sizeof(*count), 0,
                                            hipMemcpyDeviceToHost);
   return e == hipSuccess ? FXPR_OK : static_cast<int>(e);
+}
+
+extern "C" int fxpr_log_softmax_shard_max(const void* x, int x_dtype, float* row_max, int64_t rows, int64_t cols,
+                                          void* stream) {
+  if (rows < 0 || cols < 0 || rows > 0x7fffffff || cols > 0x7fffffff) return FXPR_E_SHAPE;
+  if (rows == 0) return FXPR_OK;
+  if (!row_max || (cols > 0 && !x)) return FXPR_E_ARG;
+  hipStream_t st = as_stream(stream);
+  switch (x_dtype) {
+    case FXPR_DTYPE_F16: return launch_shard_max<FXPR_DTYPE_F16>(x, row_max, rows, cols, st);
+    case FXPR_DTYPE_BF16: return launch_shard_max<FXPR_DTYPE_BF16>(x, row_max, rows, cols, st);
+    case FXPR_DTYPE_F32: return launch_shard_max<FXPR_DTYPE_F32>(x, row_max, rows, cols, st);
+    default: return FXPR_E_DTYPE;
+  }
+}
+
+extern "C" int fxpr_log_softmax_shard_sum(const void* x, int x_dtype, const float* row_max, int64_t* row_sum,
+                                          int64_t rows, int64_t cols, int int_bits, int frac_bits, void* stream) {
+  if (!valid_int_bits(int_bits) || frac_bits < 0 || frac_bits > 32) return FXPR_E_BITS;
+  if (rows < 0 || cols < 0 || rows > 0x7fffffff || cols >= (int64_t(1) << 29)) return FXPR_E_SHAPE;
+  if (rows == 0) return FXPR_OK;
+  if (!row_max || !row_sum || (cols > 0 && !x)) return FXPR_E_ARG;
+  hipStream_t st = as_stream(stream);
+  auto go = [&](auto bits_tag) -> int {
+    constexpr int B = decltype(bits_tag)::value;
+    switch (x_dtype) {
+      case FXPR_DTYPE_F16: return launch_shard_sum<FXPR_DTYPE_F16, B>(x, row_max, row_sum, rows, cols, frac_bits, st);
+      case FXPR_DTYPE_BF16:
+        return launch_shard_sum<FXPR_DTYPE_BF16, B>(x, row_max, row_sum, rows, cols, frac_bits, st);
+      case FXPR_DTYPE_F32: return launch_shard_sum<FXPR_DTYPE_F32, B>(x, row_max, row_sum, rows, cols, frac_bits, st);
+      default: return FXPR_E_DTYPE;
+    }
+  };
+  if (int_bits == 16) return go(std::integral_constant<int, 16>{});
+  if (int_bits == 32) return go(std::integral_constant<int, 32>{});
+  return go(std::integral_constant<int, 64>{});
+}
+
+extern "C" int fxpr_log_softmax_shard_finish(const void* x, int x_dtype, const float* row_max,
+                                             const int64_t* row_sum, void* y, int y_dtype, int64_t rows,
+                                             int64_t cols, int frac_bits, void* stream) {
+  if (frac_bits < 0 || frac_bits > 63) return FXPR_E_BITS;
+  if (rows < 0 || cols < 0 || rows > 0x7fffffff || cols > 0x7fffffff) return FXPR_E_SHAPE;
+  if (rows == 0 || cols == 0) return FXPR_OK;
+  if (!x || !y || !row_max || !row_sum) return FXPR_E_ARG;
+  const bool f32_out = y_dtype == FXPR_DTYPE_F32;
+  if (!f32_out && y_dtype != x_dtype) return FXPR_E_DTYPE;
+  hipStream_t st = as_stream(stream);
+  switch (x_dtype) {
+    case FXPR_DTYPE_F16:
+      return f32_out ? launch_shard_finish<FXPR_DTYPE_F16, FXPR_DTYPE_F32>(x, row_max, row_sum, y, rows, cols,
+                                                                           frac_bits, st)
+                     : launch_shard_finish<FXPR_DTYPE_F16, FXPR_DTYPE_F16>(x, row_max, row_sum, y, rows, cols,
+                                                                           frac_bits, st);
+    case FXPR_DTYPE_BF16:
+      return f32_out ? launch_shard_finish<FXPR_DTYPE_BF16, FXPR_DTYPE_F32>(x, row_max, row_sum, y, rows, cols,
+                                                                            frac_bits, st)
+                     : launch_shard_finish<FXPR_DTYPE_BF16, FXPR_DTYPE_BF16>(x, row_max, row_sum, y, rows, cols,
+                                                                             frac_bits, st);
+    case FXPR_DTYPE_F32:
+      return launch_shard_finish<FXPR_DTYPE_F32, FXPR_DTYPE_F32>(x, row_max, row_sum, y, rows, cols, frac_bits, st);
+    default: return FXPR_E_DTYPE;
+  }
 }

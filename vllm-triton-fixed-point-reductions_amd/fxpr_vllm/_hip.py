@@ -36,9 +36,14 @@ SIGNATURES: dict[str, list] = {
     "fxpr_fixed_row_sum": [_P, _I, _P, _I, _L, _L, _P],
     "fxpr_rms_norm": [_P, _P, _P, _P, _I, _L, _L, _F, _P],
     "fxpr_log_softmax": [_P, _I, _P, _I, _L, _L, _I, _I, _P],
+    "fxpr_log_softmax_shard_max": [_P, _I, _P, _L, _L, _P],
+    "fxpr_log_softmax_shard_sum": [_P, _I, _P, _P, _L, _L, _I, _I, _P],
+    "fxpr_log_softmax_shard_finish": [_P, _I, _P, _P, _P, _I, _L, _L, _I, _P],
     "fxpr_sample_greedy": [_P, _I, _L, _L, _I, _I, _I, _P, _P, _P, _P, _P],
     "fxpr_gemm": [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _P],
     "fxpr_gemm_splits": [_L, _L, _L, _I, _I],
+    "fxpr_gemm_partial": [_P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _I, _I, _P],
+    "fxpr_gemm_finish": [_P, _P, _P, _I, _L, _L, _L, _L, _I, _I, _P],
     "fxpr_unified_attention": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _I, _I, _L,
                                _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L,
                                _I, _F, _F, _I, _I, _I, _I, _P, _L, _P],

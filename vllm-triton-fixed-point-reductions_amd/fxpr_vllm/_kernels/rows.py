@@ -129,3 +129,74 @@ def log_softmax_fxp_run(x, int_bits, frac_bits, out_dtype=None):
             _hip.DTYPE_CODE[out_dtype], rows, cols, b, f, _hip.stream_ptr(x.device),
         )
     return y_2d.view(x.shape)
+
+
+# ---------------------------------------------------------------------------
+# Vocab-parallel log-softmax: each shard holds some columns of every row.
+# MAX of the shards' row maxima, then integer SUM of the shards' row sums
+# against that maximum, then each shard's outputs (the exchanges a
+# vocab-parallel lm_head needs between devices; csrc/rows.hip).
+
+
+def _shard_rows(x: torch.Tensor, what: str) -> torch.Tensor:
+    if not x.is_cuda:
+        raise RuntimeError(f"{what}: input must be CUDA")
+    if x.dtype not in _SUPPORTED_DTYPES:
+        raise TypeError(f"{what}: unsupported input dtype {x.dtype}; expected one of {_SUPPORTED_DTYPES}")
+    if x.dim() == 0:
+        raise ValueError(f"{what}: input needs a column dimension")
+    return _as_2d(x).contiguous()
+
+
+def _row_stat(t: torch.Tensor, x: torch.Tensor, dtype: torch.dtype, what: str, name: str) -> torch.Tensor:
+    if not t.is_cuda or t.dtype != dtype:
+        raise TypeError(f"{what}: {name} must be a CUDA {dtype} tensor")
+    if tuple(t.shape) != tuple(x.shape[:-1]):
+        raise ValueError(f"{what}: {name} must have shape {tuple(x.shape[:-1])}")
+    return t.contiguous()
+
+
+def log_softmax_shard_max_run(x: torch.Tensor) -> torch.Tensor:
+    """Row maxima (fp32) of this shard's columns."""
+    x_2d = _shard_rows(x, "log_softmax_fxp_shard_max")
+    out = torch.empty(x.shape[:-1], device=x.device, dtype=torch.float32)
+    rows, cols = x_2d.shape
+    if rows:
+        _hip.call("fxpr_log_softmax_shard_max", x_2d.data_ptr(), _hip.DTYPE_CODE[x.dtype], out.data_ptr(), rows,
+                  cols, _hip.stream_ptr(x.device))
+    return out
+
+
+def log_softmax_shard_sum_run(x: torch.Tensor, row_max: torch.Tensor, int_bits: int, frac_bits: int) -> torch.Tensor:
+    """Exact int64 row sums of this shard's terms against the combined maxima."""
+    what = "log_softmax_fxp_shard_sum"
+    x_2d = _shard_rows(x, what)
+    m = _row_stat(row_max, x, torch.float32, what, "row_max")
+    b, f = _bits(int_bits, frac_bits)
+    if f > 32:
+        raise ValueError(f"{what}: frac_bits above 32 can overflow the int64 row sums")
+    out = torch.empty(x.shape[:-1], device=x.device, dtype=torch.int64)
+    rows, cols = x_2d.shape
+    if rows:
+        _hip.call("fxpr_log_softmax_shard_sum", x_2d.data_ptr(), _hip.DTYPE_CODE[x.dtype], m.data_ptr(),
+                  out.data_ptr(), rows, cols, b, f, _hip.stream_ptr(x.device))
+    return out
+
+
+def log_softmax_shard_finish_run(x: torch.Tensor, row_max: torch.Tensor, row_sum: torch.Tensor, frac_bits: int,
+                                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """This shard's log-probabilities from the combined maxima and sums."""
+    what = "log_softmax_fxp_shard_finish"
+    x_2d = _shard_rows(x, what)
+    m = _row_stat(row_max, x, torch.float32, what, "row_max")
+    s = _row_stat(row_sum, x, torch.int64, what, "row_sum")
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (x.dtype, torch.float32):
+        raise TypeError(f"{what}: output dtype must be {x.dtype} or torch.float32, got {out_dtype}")
+    y = torch.empty(x_2d.shape, device=x.device, dtype=out_dtype)
+    rows, cols = x_2d.shape
+    if rows and cols:
+        _hip.call("fxpr_log_softmax_shard_finish", x_2d.data_ptr(), _hip.DTYPE_CODE[x.dtype], m.data_ptr(),
+                  s.data_ptr(), y.data_ptr(), _hip.DTYPE_CODE[out_dtype], rows, cols, int(frac_bits),
+                  _hip.stream_ptr(x.device))
+    return y.view(x.shape)

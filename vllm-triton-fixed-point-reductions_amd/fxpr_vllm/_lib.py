@@ -2,8 +2,9 @@
 
 The six reference schemas are kept verbatim (fxpr_vllm/_lib.py:13-33 of the
 reference) so callers and torch.compile graphs are a drop-in; PyTorch-ROCm
-dispatches HIP tensors through the CUDA key. Four schemas are new in this
-build: fixed_row_sum (the integer sum the reference's tests do with torch,
+dispatches HIP tensors through the CUDA key. Nine schemas are new in this
+build: the shard halves of gemm_fxp and log_softmax_fxp for more than one
+device (below), fixed_row_sum (the integer sum the reference's tests do with torch,
 _tests/test_sum.py:12-16), log_softmax_fxp (listed in the reference
 README.md:60 but not shipped), sample_greedy_fxp (the sampler of the
 reference's README.md:69, likewise not shipped) and reshape_and_cache (the
@@ -56,6 +57,23 @@ _lib.define(
 _lib.define(
     "sample_greedy_fxp(Tensor logits, int num_logprobs, int fxp_int_bits, "
     "int fxp_frac_bits) -> (Tensor, Tensor, Tensor, Tensor)"
+)
+# Shard halves for more than one device: a K-sharded (row-parallel) GEMM's
+# integer accumulators and their epilogue; a vocab-sharded log-softmax's row
+# maxima, exact row sums and outputs. Summing / maxing the shard results
+# across devices (integer all-reduces) gives the unsharded bits.
+_lib.define("gemm_fxp_partial(Tensor a, Tensor b, int fxp_int_bits, int fxp_frac_bits) -> Tensor")
+_lib.define(
+    "gemm_fxp_finish(Tensor acc, Tensor? bias, int fxp_int_bits, int fxp_frac_bits, "
+    "ScalarType out_dtype) -> Tensor"
+)
+_lib.define("log_softmax_fxp_shard_max(Tensor x) -> Tensor")
+_lib.define(
+    "log_softmax_fxp_shard_sum(Tensor x, Tensor row_max, int fxp_int_bits, int fxp_frac_bits) -> Tensor"
+)
+_lib.define(
+    "log_softmax_fxp_shard_finish(Tensor x, Tensor row_max, Tensor row_sum, int fxp_frac_bits, "
+    "ScalarType? out_dtype=None) -> Tensor"
 )
 
 
@@ -136,6 +154,33 @@ def _sample_greedy_fxp_cuda(logits: torch.Tensor, num_logprobs: int, fxp_int_bit
     return _sampling.sample_greedy_fxp_run(logits, int(num_logprobs), int(fxp_int_bits), int(fxp_frac_bits))
 
 
+def _gemm_fxp_partial_cuda(a, b, fxp_int_bits, fxp_frac_bits):
+    _check_int_bits(fxp_int_bits)
+    _check_frac_bits(fxp_frac_bits)
+    return _gemm.gemm_fxp_partial_run(a, b, int(fxp_int_bits), int(fxp_frac_bits))
+
+
+def _gemm_fxp_finish_cuda(acc, bias, fxp_int_bits, fxp_frac_bits, out_dtype):
+    _check_int_bits(fxp_int_bits)
+    _check_frac_bits(fxp_frac_bits)
+    return _gemm.gemm_fxp_finish_run(acc, bias, int(fxp_int_bits), int(fxp_frac_bits), out_dtype)
+
+
+def _log_softmax_fxp_shard_max_cuda(x):
+    return _rows.log_softmax_shard_max_run(x)
+
+
+def _log_softmax_fxp_shard_sum_cuda(x, row_max, fxp_int_bits, fxp_frac_bits):
+    _check_int_bits(fxp_int_bits)
+    _check_frac_bits(fxp_frac_bits)
+    return _rows.log_softmax_shard_sum_run(x, row_max, int(fxp_int_bits), int(fxp_frac_bits))
+
+
+def _log_softmax_fxp_shard_finish_cuda(x, row_max, row_sum, fxp_frac_bits, out_dtype=None):
+    _check_frac_bits(fxp_frac_bits)
+    return _rows.log_softmax_shard_finish_run(x, row_max, row_sum, int(fxp_frac_bits), out_dtype)
+
+
 # Register after definition so the functions stay importable by name.
 _lib.impl("float_to_fixed", _float_to_fixed_cuda, "CUDA")
 _lib.impl("fixed_to_float", _fixed_to_float_cuda, "CUDA")
@@ -147,3 +192,8 @@ _lib.impl("fixed_row_sum", _fixed_row_sum_cuda, "CUDA")
 _lib.impl("log_softmax_fxp", _log_softmax_fxp_cuda, "CUDA")
 _lib.impl("reshape_and_cache", _reshape_and_cache_cuda, "CUDA")
 _lib.impl("sample_greedy_fxp", _sample_greedy_fxp_cuda, "CUDA")
+_lib.impl("gemm_fxp_partial", _gemm_fxp_partial_cuda, "CUDA")
+_lib.impl("gemm_fxp_finish", _gemm_fxp_finish_cuda, "CUDA")
+_lib.impl("log_softmax_fxp_shard_max", _log_softmax_fxp_shard_max_cuda, "CUDA")
+_lib.impl("log_softmax_fxp_shard_sum", _log_softmax_fxp_shard_sum_cuda, "CUDA")
+_lib.impl("log_softmax_fxp_shard_finish", _log_softmax_fxp_shard_finish_cuda, "CUDA")

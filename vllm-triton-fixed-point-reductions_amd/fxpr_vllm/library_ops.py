@@ -88,7 +88,37 @@ def _reshape_and_cache_fake(key, value, kv_cache, slot_mapping):
     return None
 
 
+@torch.library.register_fake("fxpr::gemm_fxp_partial")
+def _gemm_fxp_partial_fake(a, b, fxp_int_bits, fxp_frac_bits):
+    return a.new_empty((a.shape[0], b.shape[1]), dtype=torch.int64 if int(fxp_int_bits) == 64 else torch.int32)
+
+
+@torch.library.register_fake("fxpr::gemm_fxp_finish")
+def _gemm_fxp_finish_fake(acc, bias, fxp_int_bits, fxp_frac_bits, out_dtype):
+    return acc.new_empty(acc.shape, dtype=out_dtype)
+
+
+@torch.library.register_fake("fxpr::log_softmax_fxp_shard_max")
+def _log_softmax_fxp_shard_max_fake(x):
+    return x.new_empty(x.shape[:-1], dtype=torch.float32)
+
+
+@torch.library.register_fake("fxpr::log_softmax_fxp_shard_sum")
+def _log_softmax_fxp_shard_sum_fake(x, row_max, fxp_int_bits, fxp_frac_bits):
+    return x.new_empty(x.shape[:-1], dtype=torch.int64)
+
+
+@torch.library.register_fake("fxpr::log_softmax_fxp_shard_finish")
+def _log_softmax_fxp_shard_finish_fake(x, row_max, row_sum, fxp_frac_bits, out_dtype=None):
+    return torch.empty_like(x, dtype=x.dtype if out_dtype is None else out_dtype)
+
+
 gemm_fxp = torch.ops.fxpr.gemm_fxp
+gemm_fxp_partial = torch.ops.fxpr.gemm_fxp_partial
+gemm_fxp_finish = torch.ops.fxpr.gemm_fxp_finish
+log_softmax_fxp_shard_max = torch.ops.fxpr.log_softmax_fxp_shard_max
+log_softmax_fxp_shard_sum = torch.ops.fxpr.log_softmax_fxp_shard_sum
+log_softmax_fxp_shard_finish = torch.ops.fxpr.log_softmax_fxp_shard_finish
 rms_norm_fxp = torch.ops.fxpr.rms_norm_fxp
 rms_norm_fxp_residual = torch.ops.fxpr.rms_norm_fxp_residual
 float_to_fixed = torch.ops.fxpr.float_to_fixed
