@@ -552,7 +552,6 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
 #pragma unroll
       for (int r = 0; r < 4; ++r) I[i][j][r] = 0;
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  bool out_of_range = false;  // WIDEN: a K-tile outside the rounding-constant range
 
   // Fragment reads: lane (row lane % 16 of each 16-row block, k slot kg)
   // reads chunk c = 4 h + kg of its row; the row's swizzle (row >> 1) & 7
@@ -631,25 +630,24 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       }
     }
   };
-  // Whether every partial of the wave's tile satisfies |P| < fast_lim (NaN
-  // and infinities fail: v_maximum3_f32 propagates NaN).
-  auto tile_fast = [&]() __attribute__((always_inline)) -> bool {
-    {
-      float m[4] = {0.f, 0.f, 0.f, 0.f};
+  // The running maximum of |P| over every K-tile quantised by the rounding
+  // constant (NaN-propagating): a K-tile is not checked before its
+  // quantisation (that would wait for all of the wave's MFMA chains at every
+  // K-tile); a tile whose maximum ends at or above fast_lim is recomputed
+  // exactly after the loop (or, for WIDEN, marked for the 64-bit kernel).
+  float rmax[4] = {0.f, 0.f, 0.f, 0.f};
+  auto track_row = [&](int i) {
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
+    for (int j = 0; j < NB; j += 2)
 #pragma unroll
-        for (int j = 0; j < NB; j += 2)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            asm("v_maximum3_f32 %0, |%1|, |%2|, %3"
-                : "=v"(m[r])
-                : "v"(P[i][j][r]), "v"(P[i][j + 1][r]), "v"(m[r]));
-      float mm;
-      asm("v_maximum3_f32 %0, %1, %2, %3" : "=v"(mm) : "v"(m[0]), "v"(m[1]), "v"(m[2]));
-      asm("v_maximum3_f32 %0, %1, %2, %2" : "=v"(mm) : "v"(mm), "v"(m[3]));
-      return __builtin_amdgcn_ballot_w64(!(mm < args.fast_lim)) == 0;
-    }
+      for (int r = 0; r < 4; ++r)
+        asm("v_maximum3_f32 %0, |%1|, |%2|, %3" : "=v"(rmax[r]) : "v"(P[i][j][r]), "v"(P[i][j + 1][r]), "v"(rmax[r]));
+  };
+  auto rmax_fast = [&]() -> bool {
+    float mm;
+    asm("v_maximum3_f32 %0, %1, %2, %3" : "=v"(mm) : "v"(rmax[0]), "v"(rmax[1]), "v"(rmax[2]));
+    asm("v_maximum3_f32 %0, %1, %2, %2" : "=v"(mm) : "v"(mm), "v"(rmax[3]));
+    return mm < args.fast_lim;
   };
   auto quantize = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -680,10 +678,11 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
 #pragma unroll
     for (int j = 0; j < NB; ++j) P[i][j] = zero4;
 
-  // Partial last K-tile first: masked register loads (zero past K) written
-  // in the same swizzled layout, both stages.
-  if (has_tail) {
-    const int64_t kt0 = int64_t(kt_end - 1) * 128;
+  // K-tile kt into ring slots 0 and 1 of A and B by masked register loads
+  // (zero past K), in the swizzled layout, and its partials into P: the
+  // peeled tail tile, and the exact recomputation.
+  auto stage_tile = [&](int kt) {
+    const int64_t kt0 = int64_t(kt) * 128;
     for (int e = tid; e < 2 * (BM + BN) * 8; e += BT::THREADS) {
       const int st = e / ((BM + BN) * 8), rem = e % ((BM + BN) * 8);
       const int r = rem / 8, c = rem % 8;
@@ -702,7 +701,9 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     compute(0, true);
     compute(1, false);
     __syncthreads();
-  }
+  };
+  // Partial last K-tile first.
+  if (has_tail) stage_tile(kt_end - 1);
 
   // Pipelined full K-tiles: stage s = 64 k of A in its ring slot s % NSA,
   // of B in s % NSB; each matrix's DMAs run its depth - 1 stages ahead.
@@ -738,9 +739,8 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     // to it at issue.
     lds_wait(fa0, fb0);
     // tile_start: quantise the previous K-tile's partials block by block by
-    // the rounding constant (a K-tile that fails tile_fast was quantised
-    // exactly beforehand and its partials set to zero, which the rounding
-    // constant turns into zero).
+    // the rounding constant, tracking their range (a tile with any K-tile out
+    // of range is recomputed after the loop).
     auto stage = [&](int s, auto tile_start_tag) {
       constexpr bool tile_start = decltype(tile_start_tag)::value;
       dma_group(s);
@@ -754,6 +754,7 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       auto row_prologue = [&](auto ic) {
         constexpr int i = decltype(ic)::value;
         if constexpr (tile_start) {
+          track_row(i);
 #pragma unroll
           for (int j = 0; j < NB; ++j) quantize_block_fast(i, j);
         }
@@ -805,14 +806,6 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       read_frags(s + 1, 0, fa0, fb0);
     };
     for (int s = 0; s < nst; s += 2) {
-      if (!tile_fast()) {  // rare: partials out of the fast range, NaN or infinite
-        if constexpr (WIDEN) out_of_range = true;
-        quantize();
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int j = 0; j < NB; ++j) P[i][j] = zero4;
-      }
       stage(s, std::true_type{});
       stage(s + 1, std::false_type{});
     }
@@ -820,26 +813,47 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing DMAs into unused buffers
   }
   if constexpr (WIDEN) {
-    if (!tile_fast()) out_of_range = true;  // the last K-tile
+    // the last K-tile (quantised exactly below) must fit 32-bit sums too
+#pragma unroll
+    for (int i = 0; i < MB; ++i) track_row(i);
   }
+  // a K-tile of the wave outside the rounding-constant range (or NaN / inf)
+  const bool out_of_range = __builtin_amdgcn_ballot_w64(!rmax_fast()) != 0;
   quantize();
-  __syncthreads();  // LDS is reused by the epilogue
-  if constexpr (WIDEN) {
+  __syncthreads();  // LDS is reused by the flags and the epilogue
+  {
     // the workgroup's OR of the waves' range flags through the last words of
     // the dynamic LDS (past the epilogue's area; __syncthreads_or would add
     // static LDS, and 80 KB + a few bytes no longer fits two workgroups per
-    // CU); a marked tile stores only its mark
+    // CU)
     constexpr size_t FLAGS = big_lds_bytes<BT>() - 4 * NW;
     static_assert(FLAGS >= size_t(NW) * BT::WM * (BT::WN + 8) * sizeof(T), "flags inside the epilogue's LDS");
+    static_assert(FLAGS >= size_t(B_RING) + 2 * B_SLOT, "flags past the recomputation's stages");
     int* flags = reinterpret_cast<int*>(smem_raw + FLAGS);
     if (lane == 0) flags[wave] = out_of_range ? 1 : 0;
     __syncthreads();
     int any = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) any |= flags[w];
-    if (any) {
-      if (tid == 0) static_cast<T*>(args.c)[m0 * args.scm + n0 * args.scn] = Io<DT>::store(__builtin_nanf(""));
-      return;
+    if (any) {  // rare
+      if constexpr (WIDEN) {
+        // 64-bit sums needed: the tile stores only its mark
+        if (tid == 0) static_cast<T*>(args.c)[m0 * args.scm + n0 * args.scn] = Io<DT>::store(__builtin_nanf(""));
+        return;
+      } else {
+        // recompute the tile's sums exactly, K-tile by K-tile
+        __syncthreads();  // every wave has read the flags
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) I[i][j][r] = 0;
+        for (int kt = kt_begin; kt < kt_end; ++kt) {
+          stage_tile(kt);
+          quantize();
+        }
+      }
     }
   }
 
