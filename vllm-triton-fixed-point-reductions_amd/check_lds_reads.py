@@ -21,6 +21,14 @@ to its wait; a read whose destination is copied on a branch edge (the way a
 compiler moves registers into place for a join) appears as such a copy on the
 fall-through side as well.
 
+The same scan covers inline-asm vector-memory loads into registers (the
+decode kernel's query loads, issued ahead of its first DMAs and waited for by
+an explicit vmcnt): a vector instruction touching such a load's destination
+before a vmcnt wait that covers it is reported. Only loads count towards
+vmcnt(N) covering a load (stores may complete out of order with loads; loads,
+DMAs included, complete in issue order), so vmcnt(N) covers a load once N or
+more loads were issued after it.
+
 A second scan covers every kernel of the sources: an inline-asm instruction
 that reads the result of an MFMA. The compiler inserts the wait states an
 MFMA result needs before its own instructions read it, but not before an asm
@@ -61,18 +69,47 @@ def _vregs(tok: str) -> set[int]:
     return {int(m.group(1))} if m else set()
 
 
+VMEM_LOAD = re.compile(r"^(global_load|buffer_load|flat_load|global_atomic\w*_rtn|buffer_atomic\w*_rtn)")
+
+
 def scan_kernel(lines: list[str]) -> list[str]:
-    """Early uses of pending ds_read destinations in one kernel's text."""
+    """Early uses of pending ds_read destinations (and of pending inline-asm
+    vector-memory load destinations) in one kernel's text."""
     pending: list[set[int]] = []  # LDS operations in flight, oldest first
+    vpending: list[set[int]] = []  # vector-memory loads in flight, oldest first (asm destinations only)
     found = []
+    in_asm = False
     for text in lines:
         t = text.strip()
+        if t == ";;#ASMSTART":
+            in_asm = True
+            continue
+        if t == ";;#ASMEND":
+            in_asm = False
+            continue
         if not t or t[0] in ";." or t.endswith(":"):
             continue
         op, _, rest = t.partition(" ")
-        if op == "s_waitcnt" and "lgkmcnt" in t:
-            n = int(re.search(r"lgkmcnt\((\d+)\)", t).group(1))
-            pending = pending[len(pending) - n:] if 0 < n < len(pending) else ([] if n == 0 else pending)
+        if op == "s_waitcnt":
+            if "lgkmcnt" in t:
+                n = int(re.search(r"lgkmcnt\((\d+)\)", t).group(1))
+                pending = pending[len(pending) - n:] if 0 < n < len(pending) else ([] if n == 0 else pending)
+            if "vmcnt" in t:
+                n = int(re.search(r"vmcnt\((\d+)\)", t).group(1))
+                vpending = vpending[len(vpending) - n:] if 0 < n < len(vpending) else ([] if n == 0 else vpending)
+            continue
+        if VMEM_LOAD.match(op):
+            ops = rest.split()
+            used = set()
+            for tok in ops[1:]:
+                used |= _vregs(tok)
+            vlive = set().union(*vpending) if vpending else set()
+            if used & vlive:
+                found.append(f"{t}  (in flight: v{sorted(used & vlive)})")
+            # a DMA (lds) names no destination; the compiler's own loads are
+            # waited for by the compiler
+            dest = _vregs(ops[0]) if ops and in_asm and "_lds" not in op and not rest.rstrip().endswith(" lds") else set()
+            vpending.append(dest)
             continue
         if op.startswith("ds_"):
             ops = rest.split()
@@ -84,19 +121,24 @@ def scan_kernel(lines: list[str]) -> list[str]:
             for tok in srcs:
                 used |= _vregs(tok)
             live = set().union(*pending) if pending else set()
+            if any(vpending):
+                live |= set().union(*vpending)
             if used & live:
                 found.append(f"{t}  (in flight: v{sorted(used & live)})")
             pending.append(_vregs(ops[0]) if op.startswith("ds_read") and ops else set())
             continue
         if op in ("s_branch", "s_endpgm", "s_setpc_b64"):
             pending = []  # the next instruction is reached only by a jump
+            vpending = []
             continue
-        if op.startswith("s_") or not pending:
+        if op.startswith("s_") or not (pending or any(vpending)):
             continue
         used = set()
         for tok in rest.split():
             used |= _vregs(tok)
-        live = set().union(*pending)
+        live = set().union(*pending) if pending else set()
+        if any(vpending):
+            live |= set().union(*vpending)
         if used & live:
             found.append(f"{t}  (in flight: v{sorted(used & live)})")
     return found

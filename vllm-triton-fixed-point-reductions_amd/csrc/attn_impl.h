@@ -770,11 +770,31 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, kg = lane >> 4;
   const int g = blockIdx.x % a.num_kv_heads;
-  const int r = request_by_length(a, blockIdx.x / a.num_kv_heads);
+  // (the request index is wave-uniform: its bounds are scalar loads, issued
+  // together and waited for once)
+  const int r = __builtin_amdgcn_readfirstlane(request_by_length(a, blockIdx.x / a.num_kv_heads));
   const int qt = blockIdx.y, split = blockIdx.z;
-  const int q_start = a.qsl[r];
-  const int q_len = a.qsl[r + 1] - q_start;
-  const int seq_len = a.seq_lens[r];
+  const ConstI32Ptr bt_row = (ConstI32Ptr)(a.bt + int64_t(r) * a.sbt);
+  // Without a window, with a fixed chunk count per split (or one split),
+  // the first chunk and so the pages of the first NS steps (its first K
+  // tiles) follow from the launch alone: their page entries are loaded with
+  // the request's bounds, in the same round trip, and used when the
+  // cursor's pages turn out to be these (a short chunk takes the loads
+  // again).
+  const bool spec = a.window <= 0 && (!SPLIT || a.chunks_per_split > 0);
+  const int spec_t0 = (SPLIT ? split * a.chunks_per_split : 0) * CT;
+  int spec_lb[NS], spec_pe[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    spec_lb[i] = __builtin_amdgcn_readfirstlane(
+        min(max(((spec_t0 + i) * TILE + 16 * wave) >> a.ps_shift, 0), a.max_blocks - 1));
+    spec_pe[i] = spec ? bt_row[spec_lb[i]] : 0;
+  }
+  const int q_start = ((ConstI32Ptr)a.qsl)[r];
+  const int q_end = ((ConstI32Ptr)a.qsl)[r + 1];
+  const int seq_len = ((ConstI32Ptr)a.seq_lens)[r];
+  asm volatile("" ::"s"(q_start), "s"(q_end), "s"(seq_len));
+  const int q_len = q_end - q_start;
   const int ctx = seq_len - q_len;
   const int rows_total = q_len * a.group;
   const int row0 = qt * QROWS;
@@ -796,7 +816,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   const int my_hi = SPLIT ? min(c_lo + nch, my_lo + per) : c_lo + nch;
 
   const T* Qp = static_cast<const T*>(a.q);
-  const ConstI32Ptr bt_row = (ConstI32Ptr)(a.bt + int64_t(r) * a.sbt);
   const int last_block = int(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
 
   // DMA of tile t (K or V) into stage buf: the wave moves key rows
@@ -804,11 +823,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   // .. +KPI-1, lane l row +l/CPR, slot l%CPR, i.e. chunk slot ^ swz(row).
   const T* Kc = static_cast<const T*>(a.k);
   const T* Vc = static_cast<const T*>(a.v);
-  auto page_entry = [&](int t) -> int {  // the wave's page of tile t (keys clamped)
+  auto page_index = [&](int t) -> int {  // the wave's page of tile t (keys clamped)
     const int key0 = min(t * TILE + 16 * wave, seq_len - 1);
-    const int lb = __builtin_amdgcn_readfirstlane(key0 >> a.ps_shift);
-    return bt_row[min(lb, a.max_blocks - 1)];
+    return min(__builtin_amdgcn_readfirstlane(key0 >> a.ps_shift), a.max_blocks - 1);
   };
+  auto page_entry = [&](int t) -> int { return bt_row[page_index(t)]; };
   auto dma_tile = [&](bool isv, int t, int ent, int buf) __attribute__((always_inline)) {
     const uint32_t p = uint32_t(ent < 0 ? 0 : min(ent, last_block));
 #pragma unroll
@@ -828,8 +847,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
     }
   };
 
-  // The first NS - 1 steps' DMAs go out before the Q and row-setup loads,
-  // so their latencies overlap; one wait covers both before the first step.
+  // Start-up in three round trips: the request's bounds; then the page
+  // entries of the first NS steps (scalar loads issued together) alongside
+  // the Q and row-setup loads; then the first NS - 1 steps' DMAs, issued
+  // behind the Q loads, so that a wait for all but those DMAs covers Q and
+  // the first step waits for its own tile only (one page entry per DMA and a
+  // full drain before the first step used to cost two more round trips and
+  // the pipeline's depth on every workgroup).
   auto live_lo = [&](int cc) { return max(cc * CT, t_lo); };
   auto live_hi = [&](int cc) { return min(cc * CT + CT, t_hi); };
   // the step after (cc, isv, t)
@@ -852,52 +876,75 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
   // steps of this workgroup: per chunk its live K tiles, then the same V tiles
   int total_steps = 0;
   for (int c = my_lo; c < my_hi; ++c) total_steps += 2 * (live_hi(c) - live_lo(c));
+  // Cursor states and page entries of steps 0 .. NS - 1. Past the last step
+  // the cursor stays on it, so a workgroup with fewer than NS - 1 steps
+  // issues its last tile again into stages no step reads: every workgroup
+  // issues NS - 1 steps' DMAs before its first wait.
+  bool pv[NS];
+  int pt[NS], pe[NS];
   if (my_lo < my_hi) {
-    dent = page_entry(dt);
 #pragma unroll
-    for (int i = 0; i + 1 < NS; ++i) {
-      if (i < total_steps) {
-        dma_tile(dv, dt, dent, i);
-        advance(dc_, dv, dt);
-        dent = page_entry(dt);
-      }
+    for (int i = 0; i < NS; ++i) {
+      pv[i] = dv;
+      pt[i] = dt;
+      const int lb = page_index(dt);
+      pe[i] = spec && lb == spec_lb[i] ? spec_pe[i] : bt_row[lb];
+      if (i + 1 < NS) advance(dc_, dv, dt);
     }
+    dent = pe[NS - 1];
   }
 
   // Q fragments (MFMA A operand): lane holds row lane%16, its k slots.
+  // Inline-asm loads, waited for by an asm wait tied to their registers
+  // after the first DMAs: loads the compiler sees before a loop that stores
+  // make it drain every vector-memory operation (the DMAs too) ahead of the
+  // loop. An invalid row loads token 0 (in bounds) and is zeroed after.
   u32x4 qf[QSTEPS];
+  const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + (lane & 15));
   {
-    const RowInfo qrow = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + (lane & 15));
     const T* qbase = Qp + qrow.token * a.sq_t + int64_t(qrow.head) * a.sq_h;
 #pragma unroll
-    for (int j = 0; j < QSTEPS; ++j) {
-      const int d = 32 * j + 8 * kg;
-      qf[j] = qrow.valid ? *reinterpret_cast<const u32x4*>(qbase + d) : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < QSTEPS; ++j)
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(qf[j]) : "v"(qbase + 32 * j + 8 * kg) : "memory");
   }
   // Score-layout rows 4*kg + e as valid key ranges (empty outside the request).
-  int ks[4], ke[4], qp[4];
-  float slope[4];
+  int ks[4], ke[4], qp[4], hd[4];
+  float slope[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + 4 * kg + e);
     ks[e] = ri.valid ? ri.kstart : 0x7fffffff;
     ke[e] = ri.valid ? ri.kend : 0;
     qp[e] = ri.qpos;
-    slope[e] = a.alibi ? a.alibi[ri.head] : 0.0f;
+    hd[e] = ri.head;
   }
-  if (SPLIT && split == 0 && tid < QROWS) {
-    const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
-    if (ri.valid) {
-      int* cr = a.crange + 2 * (ri.token * a.num_heads + ri.head);
-      cr[0] = c_lo;
-      cr[1] = c_lo + nch;
-    }
+  if (a.alibi) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) slope[e] = a.alibi[hd[e]];
+    // waited for here, before any DMA: a load the loop uses that is still in
+    // flight at its entry makes the compiler drain every DMA there
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   }
 
-  // Q, row setup and the first DMAs landed (an s_waitcnt the compiler sees,
-  // so it does not wait for the setup loads later behind the loop's DMAs).
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  if (my_lo < my_hi) {
+    __builtin_amdgcn_sched_barrier(0);  // the Q and row-setup loads stay ahead of the DMAs
+#pragma unroll
+    for (int i = 0; i + 1 < NS; ++i) dma_tile(pv[i], pt[i], pe[i], i);
+  }
+  // Q landed: at most the NS - 1 steps' DMAs issued behind it are still in
+  // flight (loads complete in issue order). A workgroup without chunks
+  // issues no DMAs and never reads Q; one wait without a branch keeps the
+  // compiler from copying registers of loads in flight into place for a join.
+  constexpr int kPro = (NS - 1) * G::NDMA;
+  static_assert(kPro < 64, "vmcnt field");
+  if constexpr (QSTEPS == 4)
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]) : "n"(kPro) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(qf[0]), "+v"(qf[1]) : "n"(kPro) : "memory");
+  if (!qrow.valid) {
+#pragma unroll
+    for (int j = 0; j < QSTEPS; ++j) qf[j] = u32x4{0u, 0u, 0u, 0u};
+  }
 
   // Per-lane LDS offsets within a stage.
   // K fragment j of the lane's key (row wave*16 + lane%16), chunk 4j + kg.
@@ -1126,9 +1173,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
             if (wave + 4 * b < DBLK) static_cast<AccT*>(a.wv_ws)[slot * a.head_dim + d] = wv[b][e];
           }
         }
-        // the stores count in vmcnt: let them (and the DMAs ahead) land so
-        // the next chunk's explicit waits count only its own DMAs
-        if (c + 1 < my_hi) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // No drain here. The stores count in vmcnt and may complete out of
+        // order with the loads, but the loads (DMAs included) complete in
+        // issue order. While a step's DMA is outstanding, so are the DMAs of
+        // every later step, so "at most L outstanding" with L the later
+        // steps' DMA count still implies the step's DMA landed; stores in
+        // flight only make the wait stricter. A drain here emptied the ring
+        // at every chunk boundary.
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1143,7 +1194,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dma_kernel(AttnArgs a) {
         }
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // DMAs into unused stages
+    // No wait here: the last step waited for every DMA (none is issued after
+    // it, and a wave's loads complete in issue order), so no DMA can land in
+    // the LDS after the workgroup has given it up. Its partial stores need no
+    // wait before the wave ends (waiting for them held each workgroup's CU
+    // slot for their write latency).
+  }
+
+  if (SPLIT && split == 0 && tid < QROWS) {
+    const RowInfo ri = row_info(a, g, q_start, q_len, ctx, seq_len, row0 + tid);
+    if (ri.valid) {
+      int* cr = a.crange + 2 * (ri.token * a.num_heads + ri.head);
+      cr[0] = c_lo;
+      cr[1] = c_lo + nch;
+    }
   }
 
   if constexpr (!SPLIT) {
