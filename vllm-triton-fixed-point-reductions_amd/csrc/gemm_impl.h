@@ -85,9 +85,6 @@ struct GemmArgs {
   float fast_lim;
   int ktiles, tiles_per_split, tiles_m, tiles_n;
   int c_vec;         // C rows unit-stride, 16-byte aligned (vector row stores)
-  // gemm_big_kernel: compute only the output tiles whose first element C[m0][n0]
-  // is NaN (the marks of the int32-accumulating pass of a 64-bit launch)
-  int redo_marked;
   // kPartial: write the integer accumulators to ws ([M][N], the split-K
   // layout with one split) instead of C; kFinish: only the epilogue, from the
   // accumulators in ws to C
@@ -470,8 +467,10 @@ __device__ __forceinline__ void lgkm_wait_for(u32x4& a, u32x4& b, u32x4& c, u32x
 // constant (|P * 2^f| < 2^22, so |q| < 2^22) and there are fewer than 512
 // K-tiles, the 32-bit sum cannot wrap and equals the 64-bit one; the epilogue
 // converts it as a 64-bit value. A tile with any K-tile outside that range
-// stores nothing but a NaN at C[m0][n0] for the 64-bit kernel's redo pass.
-template <int DT, int BITS, class BT, bool SPLIT, bool WIDEN = false>
+// stores nothing but a NaN at C[m0][n0] for the 64-bit kernel's REDO pass,
+// which computes exactly those tiles (a NaN there from a NaN bias costs a
+// redundant, bit-identical recompute).
+template <int DT, int BITS, class BT, bool SPLIT, bool WIDEN = false, bool REDO = false>
 __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs args) {
   using M_ = Mma<DT>;
   using T = typename M_::T;
@@ -498,12 +497,36 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS targets in SGPRs
   const int wm = wave / BT::WGN, wn = wave % BT::WGN;
   int tm, tn;
-  tile_coords(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, tm, tn);
-  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
-  if (args.redo_marked) {  // uniform: one element per workgroup
-    const float c0 = Io<DT>::load(static_cast<const T*>(args.c)[m0 * args.scm + n0 * args.scn]);
-    if (!(c0 != c0)) return;
+  [[maybe_unused]] uint64_t redo_mask = 0;
+  [[maybe_unused]] const int redo_tiles = args.tiles_m * args.tiles_n;
+  [[maybe_unused]] const int redo_base = int(blockIdx.x) * 64;
+  if constexpr (REDO) {
+    // The 64-bit pass over the tiles a WIDEN launch marked (a NaN at the
+    // tile's first element): workgroup w checks the marking launch's
+    // workgroups 64 w .. 64 w + 63 with one load per lane and runs the tile
+    // body for each marked one, in order (the body's end jumps back here).
+    // No marks (the common case): 1002 workgroups of one round of loads at
+    // M = 8192 instead of 64128 workgroups that each load their mark and exit
+    // (0.2 ms).
+    bool marked = false;
+    if (redo_base + lane < redo_tiles) {
+      tile_coords(redo_base + lane, redo_tiles, args.tiles_m, args.tiles_n, tm, tn);
+      const float c0 =
+          Io<DT>::load(static_cast<const T*>(args.c)[int64_t(tm) * BM * args.scm + int64_t(tn) * BN * args.scn]);
+      marked = c0 != c0;
+    }
+    // every wave loads the same marks: the mask is uniform over the workgroup
+    redo_mask = __builtin_amdgcn_ballot_w64(marked);
+    if (!redo_mask) return;
+  } else {
+    tile_coords(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, tm, tn);
   }
+redo_next:
+  if constexpr (REDO) {
+    tile_coords(redo_base + __builtin_ctzll(redo_mask), redo_tiles, args.tiles_m, args.tiles_n, tm, tn);
+    redo_mask &= redo_mask - 1;
+  }
+  const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
   const int split = blockIdx.y;
   const int kt_begin = split * args.tiles_per_split;
   const int kt_end = min(args.ktiles, kt_begin + args.tiles_per_split);
@@ -933,6 +956,12 @@ __global__ __launch_bounds__(BT::THREADS, BT::WPE) void gemm_big_kernel(GemmArgs
       }
     }
   }
+  if constexpr (REDO) {
+    if (redo_mask) {
+      __syncthreads();  // the epilogue's LDS before the next tile's DMAs
+      goto redo_next;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1085,7 +1114,7 @@ int launch_tile(const GemmArgs& a, int splits, hipStream_t st) {
   return launch_status();
 }
 
-template <int DT, int BITS, class BT, bool WIDEN = false>
+template <int DT, int BITS, class BT, bool WIDEN = false, bool REDO = false>
 int launch_big(GemmArgs a, int splits, hipStream_t st) {
   a.tiles_m = int(cdiv(a.M, BT::BM));
   a.tiles_n = int(cdiv(a.N, BT::BN));
@@ -1098,10 +1127,13 @@ int launch_big(GemmArgs a, int splits, hipStream_t st) {
       if (e != hipSuccess) return int(e);
       attr_done = true;
     }
-    kern<<<dim3(unsigned(a.tiles_m * a.tiles_n), unsigned(splits)), BT::THREADS, lds, st>>>(a);
+    const int64_t tiles = int64_t(a.tiles_m) * a.tiles_n;
+    kern<<<dim3(unsigned(REDO ? cdiv(tiles, 64) : tiles), unsigned(splits)), BT::THREADS, lds, st>>>(a);
     return launch_status();
   };
-  if constexpr (WIDEN) {
+  if constexpr (REDO) {
+    return go(gemm_big_kernel<DT, BITS, BT, false, false, true>);
+  } else if constexpr (WIDEN) {
     return go(gemm_big_kernel<DT, BITS, BT, false, true>);
   } else {
     if (splits > 1 || a.mode == kPartial) return go(gemm_big_kernel<DT, BITS, BT, true>);
@@ -1199,9 +1231,7 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
       if (full && splits <= 1 && a.ktiles < 512 && a.fast_lim >= 4.0f) {
         const int rc = launch_big<DT, 32, TB2, true>(a, 1, st);
         if (rc != FXPR_OK) return rc;
-        GemmArgs b = a;
-        b.redo_marked = 1;
-        return launch_big<DT, BITS, TB64>(b, 1, st);
+        return launch_big<DT, BITS, TB64, false, true>(a, 1, st);
       }
       return launch_big<DT, BITS, TB64>(a, splits, st);
     }
