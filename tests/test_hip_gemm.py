@@ -252,6 +252,26 @@ def test_gemm_int64_marked_tile_redo(dtype, M):
     assert not report, report
 
 
+def test_gemm_int64_redo_groups():
+    # The 64-bit redo pass checks the marking launch's tiles 64 per
+    # workgroup: 8 x 65 = 520 tiles here (nine groups, the last of 8 tiles),
+    # marks in several groups and several per group (NaN bias columns in
+    # column tiles 0, 31, 64; out-of-range K-tiles in one row tile), and
+    # every tile must equal the 64-bit kernel's (split launches) bit for bit
+    g = torch.Generator("cpu").manual_seed(1234)
+    M, K, N = 1024, 512, 8320
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = (torch.randn(K, N, generator=g) * 0.05).to(torch.bfloat16)
+    a[300:310, 0:128] = (a[300:310, 0:128].float() * 1e5).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    for col in (5, 31 * 128 + 7, 64 * 128 + 1):
+        bias[col] = float("nan")
+    full = _run(a, b, bias, bits=64, frac=16, b_layout="nk", split_k=1)
+    ref = _run(a, b, bias, bits=64, frac=16, b_layout="nk", split_k=2)
+    assert nan_aware_equal(full, ref), mismatch_report(full, ref)
+    assert torch.isnan(full[:, 5]).all() and not torch.isnan(full[:, 6]).any()
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M", [1, 5, 16])
 def test_gemm_decode_shape_kernel_matches_split_path(dtype, M):
