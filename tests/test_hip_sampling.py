@@ -75,6 +75,28 @@ def test_special_rows():
         assert ids.tolist()[1:] == [100, 0, 5, 0, 0]
 
 
+def test_top_keys_held_by_few_threads():
+    # The kernel keeps each thread's two largest keys and rescans a thread's
+    # elements when it supplies a third winner. Rows whose top 64 lie in a
+    # few threads' elements: a flat row (keys ordered by index: the first 64
+    # elements), the top 64 values in one thread's chunks of 8 (thread 3 of
+    # 512, chunks 3 + 512 i) in descending order, the same interleaved over
+    # two threads with ties, and at the row's end.
+    V = 128_256
+    x = torch.round(torch.randn(4, V, generator=torch.Generator("cpu").manual_seed(9)) * 2)
+    x[0] = 7.0
+    pos = torch.tensor([8 * (3 + 512 * i) + j for i in range(8) for j in range(8)])
+    x[1, pos] = 200.0 - torch.arange(64, dtype=torch.float32)
+    pos2 = torch.tensor([8 * (t + 512 * i) + j for i in range(4) for t in (3, 4) for j in range(8)])
+    x[2, pos2] = 150.0 - (torch.arange(64) // 3).to(torch.float32)
+    x[3, V - 64:] = 100.0
+    for dtype in (torch.bfloat16, torch.float32):
+        ids = _check(x.to(dtype), 64, 32, 16)[2].cpu()
+        assert ids[0].tolist() == list(range(64))
+        assert ids[1].tolist() == pos.tolist()
+        assert ids[3].tolist() == list(range(V - 64, V))
+
+
 def test_logprobs_equal_log_softmax_and_tokens_equal_argmax():
     x = _logits(32, 128_256, seed=11).to(DEV)
     ids, lp, top, top_lp = torch.ops.fxpr.sample_greedy_fxp(x, 20, 32, 16)

@@ -10,9 +10,14 @@
 // One workgroup per row, the row held in registers as in the log-softmax.
 // Selection is by rounds: each round takes the largest 64-bit order key
 // below the previous round's, key = order(value) << 32 | (0xfffffffe - j),
-// which makes every key of a row distinct and never all ones. A round costs
-// one pass over the thread's elements and one workgroup maximum (one barrier,
-// shared slots alternating between rounds).
+// which makes every key of a row distinct, never all ones and never zero.
+// One pass keeps each thread's two largest keys (branchless); a round is
+// then one workgroup maximum over the threads' heads (one barrier, shared
+// slots alternating between rounds), after which only the winning thread
+// moves on: its second key becomes its head, and a thread that has given up
+// both rescans its elements for the next two below the round's key (rare).
+// The first form took every round as a full pass over every element: 5
+// rounds over a 128256-wide row cost ~150 us per call.
 
 #include "rows_impl.h"
 
@@ -56,28 +61,50 @@ __global__ __launch_bounds__(kLsmThreads) void sample_greedy_kernel(
   XV keep[NREG];
   const float lse = row_lse<XDT, VEC, NREG, BITS, WIDE>(xr, keep, nchunks, frac, inv_scale, fast_sum, fred, ired);
 
-  uint64_t bound = ~uint64_t(0);   // this round takes the largest key below it
-  for (int r = 0; r < rounds; ++r) {
-    uint64_t best = 0;               // below every key
+  // the thread's two largest keys below `below` (0: none; keys are never 0)
+  uint64_t h1 = 0, h2 = 0;
+  auto scan = [&](uint64_t below) {
+    h1 = 0;
+    h2 = 0;
+    // keys and indices computed afresh each scan: the empty asm "changing"
+    // the row and the thread index keeps the compiler from hoisting every
+    // element's 64-bit key out of the rounds (hundreds of live registers)
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    if constexpr (VEC > 1) {
+#pragma unroll
+      for (int i = 0; i < NREG; ++i) asm volatile("" : "+v"(keep[i].v));
+    }
     auto consider = [&](int64_t c, const XV& xv) {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
-        const uint64_t key = order_key(Io<XDT>::load(xv.v[j]), c * VEC + j);
-        best = (key < bound && key > best) ? key : best;
+        uint64_t key = order_key(Io<XDT>::load(xv.v[j]), c * VEC + j);
+        key = key < below ? key : 0;
+        const bool gt1 = key > h1, gt2 = key > h2;
+        h2 = gt1 ? h1 : (gt2 ? key : h2);
+        h1 = gt1 ? key : h1;
       }
     };
 #pragma unroll
     for (int i = 0; i < NREG; ++i) {
-      const int64_t c = tid + static_cast<int64_t>(i) * nthr;
+      const int64_t c = t + static_cast<int64_t>(i) * nthr;
       if (c < nchunks) consider(c, keep[i]);
     }
-    for (int64_t c = tid + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) consider(c, xr[c]);
-    best = wave_max(best);
+    for (int64_t c = t + static_cast<int64_t>(NREG) * nthr; c < nchunks; c += nthr) consider(c, xr[c]);
+  };
+  scan(~uint64_t(0));
+
+  for (int r = 0; r < rounds; ++r) {
+    uint64_t best = wave_max(h1);
     if (lane == 0) kred[r & 1][wave] = best;
     __syncthreads();
     best = kred[r & 1][0];
     for (int w = 1; w < nwaves; ++w) best = best > kred[r & 1][w] ? best : kred[r & 1][w];
-    bound = best;
+    if (h1 == best && best != 0) {  // the winner (keys are distinct): its next key below best
+      h1 = h2;
+      h2 = 0;
+      if (h1 == 0 && r + 1 < rounds) scan(best);
+    }
     if (tid == 0 && best != 0) {   // k <= cols, so every round finds a key
       const int64_t j = static_cast<int64_t>(0xfffffffeu - static_cast<uint32_t>(best));
       const float lp = __fsub_rn(Io<XDT>::load(xrow[j]), lse);
