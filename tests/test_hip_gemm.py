@@ -75,18 +75,23 @@ def test_gemm_tolerance_vs_oracle(dtype, M, K, N):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_gemm_split_and_layout_invariance(dtype):
+    # split counts that the reduce kernel takes in batches of 8 and 4 splits
+    # and singly; M x N = 48 x 520 takes its 16-byte loads, 47 x 519 (not a
+    # multiple of 4 elements) its element loads
     g = torch.Generator("cpu").manual_seed(5)
     a = torch.randn(48, 2048 + 40, generator=g).to(dtype)
     b = torch.randn(2048 + 40, 520, generator=g).to(dtype)
     bias = torch.randn(520, generator=g).to(dtype)
-    ref = _run(a, b, bias, split_k=1)
-    for s in (0, 2, 3, 4, 7, 16, 64):
-        for layout in ("kn", "nk"):
-            for bits in (32,):
-                got = _run(a, b, bias, split_k=s, b_layout=layout, bits=bits)
-                assert torch.equal(got, ref), (s, layout, mismatch_report(got, ref))
-    ref64 = _run(a, b, bias, split_k=1, bits=64)
-    assert torch.equal(_run(a, b, bias, split_k=5, bits=64, b_layout="nk"), ref64)
+    for m, n in ((48, 520), (47, 519)):
+        am, bn, biasn = a[:m], b[:, :n], bias[:n]
+        ref = _run(am, bn, biasn, split_k=1)
+        for s in (0, 2, 3, 4, 7, 13, 16, 64):
+            for layout in ("kn", "nk"):
+                got = _run(am, bn, biasn, split_k=s, b_layout=layout, bits=32)
+                assert torch.equal(got, ref), (m, n, s, layout, mismatch_report(got, ref))
+        ref64 = _run(am, bn, biasn, split_k=1, bits=64)
+        for s in (5, 12):
+            assert torch.equal(_run(am, bn, biasn, split_k=s, bits=64, b_layout="nk"), ref64), (m, n, s)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

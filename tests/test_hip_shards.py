@@ -79,6 +79,21 @@ def test_k_sharded_gemm_wraps_like_the_accumulator():
         assert torch.equal(got, want), bits
 
 
+def test_gemm_finish_from_unaligned_accumulators():
+    # accumulators at a 4-byte offset (the finish takes element loads) and
+    # 7 x 13 of them (not a multiple of 4)
+    g = torch.Generator("cpu").manual_seed(8)
+    a = torch.randn(7, 256, generator=g).to(torch.bfloat16).to(DEV)
+    b = (torch.randn(256, 13, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    want = torch.ops.fxpr.gemm_fxp(a, b, None, 32, 16)
+    acc = torch.ops.fxpr.gemm_fxp_partial(a, b, 32, 16)
+    store = torch.zeros(acc.numel() + 1, dtype=torch.int32, device=DEV)
+    shifted = store[1:].view(7, 13)
+    shifted.copy_(acc)
+    assert shifted.data_ptr() % 16 != 0
+    assert torch.equal(torch.ops.fxpr.gemm_fxp_finish(shifted, None, 32, 16, torch.bfloat16), want)
+
+
 def test_gemm_partial_errors_and_empty():
     a = torch.zeros(4, 256, dtype=torch.bfloat16, device=DEV)
     b = torch.zeros(256, 8, dtype=torch.bfloat16, device=DEV)

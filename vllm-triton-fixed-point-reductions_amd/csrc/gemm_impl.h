@@ -379,20 +379,82 @@ __global__ __launch_bounds__(kThreads) void gemm_fxp_kernel(GemmArgs args) {
 }
 
 // Sum the per-split integer partials (wrapping b-bit) and apply the epilogue.
+// A thread takes kReduceVec consecutive elements of [M][N]: with vec (M * N
+// a multiple of kReduceVec and a 16-byte aligned workspace) as 16-byte
+// non-temporal loads (two for 64-bit sums), the loads of eight splits in
+// flight together; otherwise element by element.
+constexpr int kReduceVec = 4;
 template <int DT, int BITS>
-__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, int splits) {
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, int splits, int vec) {
   using T = typename Io<DT>::T;
   using AccT = typename Acc<BITS>::T;
-  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  constexpr int V = kReduceVec;
   const int64_t MN = args.M * args.N;
-  if (idx >= MN) return;
+  const int64_t e0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * V;
+  if (e0 >= MN) return;
   const AccT* ws = static_cast<const AccT*>(args.ws);
-  AccT acc = 0;
-  for (int s = 0; s < splits; ++s) acc = wrap_add<BITS>(acc, ws[int64_t(s) * MN + idx]);
-  const int64_t m = idx / args.N, n = idx % args.N;
-  float v = acc_to_f32<BITS>(acc, args.inv_scale);
-  if (args.bias) v = __fadd_rn(v, args.bias[n]);
-  static_cast<T*>(args.c)[m * args.scm + n * args.scn] = Io<DT>::store(v);
+  AccT acc[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc[e] = 0;
+  if (vec) {
+    constexpr int NL = V * int(sizeof(AccT)) / 16;  // 16-byte loads per split
+    constexpr int G = 8;                            // splits per batch of loads
+    auto add = [&](const u32x4 (&w)[NL]) {
+#pragma unroll
+      for (int l = 0; l < NL; ++l) {
+        if constexpr (BITS == 64) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            acc[2 * l + h] =
+                wrap_add<BITS>(acc[2 * l + h], int64_t(uint64_t(w[l][2 * h]) | (uint64_t(w[l][2 * h + 1]) << 32)));
+        } else {
+#pragma unroll
+          for (int h = 0; h < 4; ++h) acc[h] = wrap_add<BITS>(acc[h], int32_t(w[l][h]));
+        }
+      }
+    };
+    auto load = [&](int s, u32x4 (&w)[NL]) {
+      const u32x4* p = reinterpret_cast<const u32x4*>(ws + int64_t(s) * MN + e0);
+#pragma unroll
+      for (int l = 0; l < NL; ++l) w[l] = __builtin_nontemporal_load(p + l);
+    };
+    auto batch = [&](int s, auto n_tag) {
+      constexpr int n = decltype(n_tag)::value;
+      u32x4 w[n][NL];
+#pragma unroll
+      for (int g = 0; g < n; ++g) load(s + g, w[g]);
+#pragma unroll
+      for (int g = 0; g < n; ++g) add(w[g]);
+    };
+    int s = 0;
+    for (; s + G <= splits; s += G) batch(s, std::integral_constant<int, G>{});
+    if (s + G / 2 <= splits) {
+      batch(s, std::integral_constant<int, G / 2>{});
+      s += G / 2;
+    }
+    for (; s < splits; ++s) {
+      u32x4 w[NL];
+      load(s, w);
+      add(w);
+    }
+  } else {
+    for (int s = 0; s < splits; ++s)
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        if (e0 + e < MN) acc[e] = wrap_add<BITS>(acc[e], ws[int64_t(s) * MN + e0 + e]);
+  }
+  int64_t m = e0 / args.N, n = e0 % args.N;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    if (e0 + e >= MN) break;
+    float v = acc_to_f32<BITS>(acc[e], args.inv_scale);
+    if (args.bias) v = __fadd_rn(v, args.bias[n]);
+    static_cast<T*>(args.c)[m * args.scm + n * args.scn] = Io<DT>::store(v);
+    if (++n == args.N) {
+      n = 0;
+      ++m;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1262,7 +1324,8 @@ int run_gemm(GemmArgs a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
     if (rc != FXPR_OK || splits <= 1 || a.mode == kPartial) return rc;
   }
   const int64_t mn = a.M * a.N;
-  gemm_splitk_reduce_kernel<DT, BITS><<<dim3(unsigned(cdiv(mn, 256))), 256, 0, st>>>(a, splits);
+  const int rvec = mn % kReduceVec == 0 && (reinterpret_cast<uintptr_t>(a.ws) & 15) == 0;
+  gemm_splitk_reduce_kernel<DT, BITS><<<dim3(unsigned(cdiv(mn, 256 * kReduceVec))), 256, 0, st>>>(a, splits, rvec);
   return launch_status();
 }
 
