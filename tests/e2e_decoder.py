@@ -85,12 +85,20 @@ class Decoder:
         c = self.cfg
         return torch.ops.fxpr.gemm_fxp(x, w.t(), None, c.int_bits, c.frac_bits)
 
-    def _rope(self, x, pos):  # x [T, H, D], rotate-half, fp32 math per element
+    def _rope_tables(self, pos):  # once per step: [T, 1, D] cos and signed sin
         ang = pos.to(torch.float32)[:, None] * self.inv_freq[None, :]
-        cos, sin = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+        cos, sin = torch.cos(ang), torch.sin(ang)
+        return torch.cat([cos, cos], -1)[:, None, :], torch.cat([-sin, sin], -1)[:, None, :]
+
+    def _rope(self, x, tables):  # x [T, H, D], rotate-half, fp32 math per element
+        # x1 cos - x2 sin | x2 cos + x1 sin: each product rounded, then one
+        # add (x2 * -sin is exactly -(x2 * sin)); q and k heads in one call
+        cos, sin = tables
+        T, H, D = x.shape
         xf = x.float()
-        x1, x2 = xf[..., : x.shape[-1] // 2], xf[..., x.shape[-1] // 2:]
-        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
+        out = xf * cos
+        out += xf.view(T, H, 2, D // 2).flip(2).reshape(T, H, D) * sin
+        return out.to(x.dtype)
 
     def step(self, tokens, positions, qsl, seq_lens, block_table, slots, max_q, sample_rows):
         """One forward over a flat batch. Returns, for the token rows
@@ -100,6 +108,7 @@ class Decoder:
         T = tokens.shape[0]
         h = self.embed[tokens]
         residual = None
+        rope = self._rope_tables(positions)
         for li, L in enumerate(self.layers):
             if residual is None:
                 residual = h.clone()
@@ -108,21 +117,22 @@ class Decoder:
                 x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, L["ln1"], c.eps)
             qkv = self._gemm(x, L["wqkv"])
             nq, nkv = c.heads * c.head_dim, c.kv_heads * c.head_dim
-            q = self._rope(qkv[:, :nq].view(T, c.heads, c.head_dim), positions)
-            k = self._rope(qkv[:, nq:nq + nkv].view(T, c.kv_heads, c.head_dim), positions)
+            qk = self._rope(qkv[:, :nq + nkv].view(T, c.heads + c.kv_heads, c.head_dim), rope)
+            q, k = qk[:, :c.heads], qk[:, c.heads:]
             v = qkv[:, nq + nkv:].view(T, c.kv_heads, c.head_dim)
             torch.ops.fxpr.reshape_and_cache(k, v, self.kv[li], slots)
-            o = torch.empty_like(q)
+            o = torch.empty(T, c.heads, c.head_dim, dtype=q.dtype, device=q.device)
             torch.ops.fxpr.unified_attention_fxp(q, self.kv[li], o, qsl, seq_lens, block_table, max_q, None,
                                                  True, c.head_dim ** -0.5, c.int_bits, c.frac_bits, 0.0, 0, 0)
-            del q, k, v, qkv
+            del q, k, v, qk, qkv
             h = self._gemm(o.view(T, -1), L["wo"])
             x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, L["ln2"], c.eps)
             gu = self._gemm(x, L["wgu"])
-            act = torch.nn.functional.silu(gu[:, :c.ffn].float())
-            act.mul_(gu[:, c.ffn:].float())
+            guf = gu.float()
+            act = torch.nn.functional.silu(guf[:, :c.ffn])
+            act.mul_(guf[:, c.ffn:])
             h = self._gemm(act.to(c.dtype), L["wd"])
-            del act, gu
+            del act, gu, guf
         x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, self.ln_f, c.eps)
         logits = self._gemm(x[sample_rows].contiguous(), self.lm_head)
         ids, lp, top, top_lp = torch.ops.fxpr.sample_greedy_fxp(logits, c.num_logprobs, c.int_bits, c.frac_bits)
