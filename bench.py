@@ -235,7 +235,7 @@ def wl_gemm(steps, warmup, M, N=128256, K=4096, dtype_name="bf16", int_bits=32, 
     res = {"workload": f"gemm_fxp {dtype_name} A[{M},{K}] x B[{K},{N}] (B K-contiguous) "
                        f"Q{frac_bits}/i{int_bits}",
            "ms": round(ms, 5), "flops": flops, "bytes": nbytes,
-           "splits": KG.resolve_split_k(M, N, K, dtype, split_k),
+           "splits": KG.resolve_split_k(M, N, K, dtype, int_bits, split_k),
            "mfma": mfma_roofline(flops, ms, peak), "hbm": hbm_roofline(nbytes, ms)}
     # the bounding roofline: HBM for skinny M, MFMA from the ridge point on
     res["roofline"] = res["mfma"] if flops / nbytes > peak * 1e12 / (HBM_PEAK_GBS * 1e9) else res["hbm"]

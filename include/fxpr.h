@@ -221,10 +221,11 @@ int fxpr_gemm_finish(const void* acc, const float* bias, void* c,
                      int64_t stride_cn, int int_bits, int frac_bits,
                      void* stream);
 
-/* Split count fxpr_gemm will use for this shape and request.
- * Host-side policy of the reference: _resolve_split_k (gemm.py:385-412). */
+/* Split count fxpr_gemm will use for this shape, accumulator width and
+ * request. Host-side policy of the reference: _resolve_split_k
+ * (gemm.py:385-412), which takes the accumulator width too. */
 int fxpr_gemm_splits(int64_t m, int64_t n, int64_t k, int io_dtype,
-                     int split_k);
+                     int int_bits, int split_k);
 
 /* Workspace bytes fxpr_gemm needs for this shape and request (0 = none).
  * Replaces the persistent scratch of gemm.py:61-107. */

@@ -166,6 +166,43 @@ def test_gemm_big_rounding_constant_ties(dtype, M, bits, frac, K):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [17, 32, 48, 64])
+def test_gemm_big_64x256_tiles_exact(dtype, M):
+    # M = 17 .. 64 with 16- / 32-bit sums: 64 x 256 tiles (N = 520: three
+    # column tiles, the last ragged). Dyadic inputs keep every K-tile dot
+    # exact, so the result equals the oracle bit for bit: ties of the
+    # rounding-constant path (K = 300: the peeled partial last K-tile), K-tiles
+    # beyond the fast range (exact path), non-finite partials, and split
+    # launches equal to the unsplit one
+    g = torch.Generator("cpu").manual_seed(300 + M)
+    N = 520
+    for K in (300, 640):
+        for bits, frac in ((32, 16), (16, 8), (32, 8)):
+            u = (frac + 1) // 2
+            a = _dyadic((M, K), -8, 8, -u, g, dtype)
+            b = _dyadic((K, N), -8, 8, -(frac + 1 - u), g, dtype)
+            got = _run(a, b, bits=bits, frac=frac, b_layout="nk")
+            want = _oracle(a, b, None, bits, frac)
+            assert torch.equal(got, want), (K, bits, frac, mismatch_report(got, want))
+            for s in (2, 3):
+                assert torch.equal(_run(a, b, bits=bits, frac=frac, b_layout="nk", split_k=s), want), (K, bits, s)
+    K = 512
+    a = _dyadic((M, K), -2, 2, -6, g, dtype)
+    b = _dyadic((K, N), -2, 2, 0, g, dtype)
+    a[M // 2, 128:256] *= 256  # one row's second K-tile beyond the fast range
+    a[3, 0:128] *= 256
+    a[1, 10] = float("inf")
+    a[M - 1, 300] = float("nan")
+    b[17, 9] = float("nan")
+    for bits in (32, 16):
+        frac = 8 if bits == 16 else 16
+        want = _oracle(a, b, None, bits, frac)
+        for s in (1, 4):
+            got = _run(a, b, bits=bits, frac=frac, b_layout="nk", split_k=s)
+            assert torch.equal(got, want), (bits, s, mismatch_report(got, want))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M", _BIG_M)
 def test_gemm_big_mixed_tile_paths(dtype, M):
     # some waves' K-tiles hold partials beyond the fast range (|P| up to 2048

@@ -83,8 +83,8 @@ def test_attention_policy_is_static(lib):
 BF16, F16, F32 = 1, 0, 2
 
 
-def gemm_splits(lib, m, n, k, dt=BF16, requested=0):
-    return lib.fxpr_gemm_splits(m, n, k, dt, requested)
+def gemm_splits(lib, m, n, k, dt=BF16, requested=0, bits=32):
+    return lib.fxpr_gemm_splits(m, n, k, dt, bits, requested)
 
 
 def test_gemm_explicit_request_wins(lib):
@@ -111,14 +111,21 @@ def test_gemm_auto_decode_shapes_stream(lib):
 
 def test_gemm_auto_split_fills_the_gpu(lib):
     # elsewhere: 512 / (output tiles) splits, at most 16, when the tiles do
-    # not reach 256 (16 x 256 tiles for M <= 16, 128 x 128 from M = 17)
+    # not reach 256 (16 x 256 tiles for M <= 16; from M = 17 to 64 64 x 256
+    # with 16- / 32-bit sums and 128 x 128 with 64-bit ones; 128 x 128 from
+    # M = 65)
     assert gemm_splits(lib, 16, 8193, 4096) == 15        # 33 tiles
     assert gemm_splits(lib, 1, 28672, 4096) == 4         # 112 tiles
     assert gemm_splits(lib, 1, 128256, 4096) == 1        # 501 tiles
-    assert gemm_splits(lib, 32, 4096, 4096) == 16        # 32 tiles
-    assert gemm_splits(lib, 32, 28672, 4096) == 2        # 224 tiles
+    assert gemm_splits(lib, 32, 4096, 4096) == 16        # 16 tiles
+    assert gemm_splits(lib, 32, 6144, 4096) == 16        # 24 tiles
+    assert gemm_splits(lib, 32, 28672, 4096) == 4        # 112 tiles
+    assert gemm_splits(lib, 64, 28672, 4096, bits=16) == 4
+    assert gemm_splits(lib, 32, 28672, 4096, bits=64) == 2    # 224 tiles
+    assert gemm_splits(lib, 32, 6144, 4096, bits=64) == 10    # 48 tiles
+    assert gemm_splits(lib, 65, 28672, 4096) == 2        # 224 tiles
     assert gemm_splits(lib, 256, 4096, 4096) == 8        # 64 tiles
-    assert gemm_splits(lib, 32, 128256, 4096) == 1       # 1002 tiles
+    assert gemm_splits(lib, 32, 128256, 4096) == 1       # 501 tiles
     assert gemm_splits(lib, 8192, 128256, 4096) == 1
     assert gemm_splits(lib, 32, 4096, 256) == 2          # capped at the 2 K-tiles
     # fp32 inputs keep the skinny tiles (16 / 32 / 64 x 256) and 64-wide K-tiles

@@ -5,15 +5,15 @@
 using namespace fxpr;
 using namespace fxpr::gemm;
 
-extern "C" int fxpr_gemm_splits(int64_t m, int64_t n, int64_t k, int io_dtype, int split_k) {
+extern "C" int fxpr_gemm_splits(int64_t m, int64_t n, int64_t k, int io_dtype, int int_bits, int split_k) {
   if (m <= 0 || n <= 0 || k < 0) return 1;
-  return resolve_splits(m, n, k, io_dtype, split_k);
+  return resolve_splits(m, n, k, io_dtype, int_bits, split_k);
 }
 
 extern "C" int64_t fxpr_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int io_dtype,
                                              int int_bits, int split_k) {
   if (m <= 0 || n <= 0 || k < 0) return 0;
-  return ws_bytes_for(m, n, int_bits, resolve_splits(m, n, k, io_dtype, split_k));
+  return ws_bytes_for(m, n, int_bits, resolve_splits(m, n, k, io_dtype, int_bits, split_k));
 }
 
 namespace {
@@ -64,7 +64,7 @@ int gemm_launch(const void* a, const void* b, const float* bias, void* c, int io
   } else {
     return FXPR_E_ARG;  // B needs one unit-stride dimension
   }
-  const int splits = mode == kPartial ? 1 : resolve_splits(m, n, k, io_dtype, split_k);
+  const int splits = mode == kPartial ? 1 : resolve_splits(m, n, k, io_dtype, int_bits, split_k);
   if (splits > 1 && (!workspace || workspace_bytes < ws_bytes_for(m, n, int_bits, splits)))
     return FXPR_E_WORKSPACE;
   if (k > 0 && cdiv(k, ktile_for(io_dtype)) > 0x7fffffff) return FXPR_E_SHAPE;

@@ -464,8 +464,9 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs args, 
 // identical to every other configuration; only the schedule differs.
 //
 // Waves of 64 x 64 outputs, two per SIMD: two 4-wave workgroups per CU over
-// 128 x 128 tiles (the two waves of a SIMD belong to different workgroups and
-// never wait on the same barrier); with 64-bit sums one wave per SIMD.
+// 128 x 128 tiles, or 64 x 256 ones at M <= 64 (the two waves of a SIMD
+// belong to different workgroups and never wait on the same barrier); with
+// 64-bit sums one wave per SIMD.
 // A and B stages (64 k) go straight from global memory into LDS with
 // global_load_lds_dwordx4 (no staging registers).
 // Rows are 128 B with the 16-byte chunk c of row r stored at slot
@@ -500,6 +501,13 @@ using TB2 = BigTile<128, 128, 2, 2, 2, FXPR_TB2_NSB>;
 // registers of it): one wave per SIMD, one 4-wave workgroup per CU; A two
 // stages deep, B three (2 % over three of each)
 using TB64 = BigTile<128, 128, 2, 2, 2, 3, 1>;
+// M = 17 .. 64 with 16- / 32-bit sums: one row of four 64 x 64 waves over 256
+// columns, A and B two stages deep (80 KB: two workgroups per CU). A 128-row
+// tile computes 2-4x the MFMAs those rows need and moves 2-4x their A:
+// graph-timed at M = 32, K = 4096, N = 28672 / 4096 / 6144 and the lm_head:
+// 65.1 / 18.5 / 23.2 / 226.7 -> 53.3 / 17.2 / 21.9 / 181.5 us.
+using TS64 = BigTile<64, 256, 1, 4, 2, 2>;
+inline bool ts64_rows(int64_t M, int bits) { return M > 16 && M <= 64 && bits != 64; }
 
 template <class BT> constexpr size_t big_lds_bytes() {
   constexpr size_t stages = (size_t(BT::NSA) * BT::BM + size_t(BT::NSB) * BT::BN) * 128;
@@ -911,9 +919,13 @@ redo_next:
     // the dynamic LDS (past the epilogue's area; __syncthreads_or would add
     // static LDS, and 80 KB + a few bytes no longer fits two workgroups per
     // CU)
-    constexpr size_t FLAGS = big_lds_bytes<BT>() - 4 * NW;
-    static_assert(FLAGS >= size_t(NW) * BT::WM * (BT::WN + 8) * sizeof(T), "flags inside the epilogue's LDS");
-    static_assert(FLAGS >= size_t(B_RING) + 2 * B_SLOT, "flags past the recomputation's stages");
+    // (past the recomputation's two stages where they fit there; otherwise
+    // right past the epilogue's area: the recomputation starts only after a
+    // barrier that follows every wave's read of the flags)
+    constexpr size_t EPI = size_t(NW) * BT::WM * (BT::WN + 8) * sizeof(T);
+    constexpr size_t LAST = big_lds_bytes<BT>() - 4 * NW;
+    constexpr size_t FLAGS = LAST >= size_t(B_RING) + 2 * B_SLOT ? LAST : (EPI + 15) / 16 * 16;
+    static_assert(FLAGS >= EPI && FLAGS + 4 * NW <= big_lds_bytes<BT>(), "flags past the epilogue's LDS");
     int* flags = reinterpret_cast<int*>(smem_raw + FLAGS);
     if (lane == 0) flags[wave] = out_of_range ? 1 : 0;
     __syncthreads();
@@ -1271,9 +1283,10 @@ template <int DT, int BITS>
 int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipStream_t st) {
   const TileId t = pick_tile(a.M);
   // gemm_big_kernel's 32-bit lane offsets span up to 256 rows of A or B.
-  // From M = 17 its 128 x 128 tiles (rows past M clamped, never stored) beat
-  // the skinny tiles: 183 / 187 us against 215 / 244 at M = 32 / 64 (64-bit
-  // sums: 189 / 192 against 245 / 362); at M <= 16 the skinny tile streams B
+  // From M = 17 its tiles (rows past M clamped, never stored) beat the skinny
+  // tiles: 183 / 187 us against 215 / 244 at M = 32 / 64 on the lm_head with
+  // 128 x 128 tiles (64-bit sums: 189 / 192 against 245 / 362), and the
+  // 64 x 256 ones of M <= 64 more; at M <= 16 the skinny tile streams B
   // faster (153 against 176 us).
   const bool big_ok = vec && !b_ncontig && big_rows(a.M) && a.lda <= (int64_t(1) << 22) &&
                       a.ldb <= (int64_t(1) << 22);
@@ -1299,6 +1312,7 @@ int dispatch_tile(const GemmArgs& a, bool b_ncontig, bool vec, int splits, hipSt
     }
   }
   if constexpr (DT != FXPR_DTYPE_F32 && BITS != 64) {
+    if (big_ok && ts64_rows(a.M, BITS)) return launch_big<DT, BITS, TS64>(a, splits, st);
     if (big_ok) return launch_big<DT, BITS, TB2>(a, splits, st);
   }
   if (vec && !b_ncontig) {
@@ -1333,9 +1347,10 @@ inline int ktile_for(int io_dtype) { return io_dtype == FXPR_DTYPE_F32 ? 64 : 12
 
 // Split count: explicit request wins (clamped to the K-tile count);
 // otherwise none for the shapes of the decode-shape kernel (16-bit, M <= 16,
-// N <= 8192), and elsewhere a split only when the output tiles cannot fill
-// the 256 CUs about twice: 512 / tiles splits, at most 16.
-inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int requested) {
+// N <= 8192), and elsewhere a split only when the output tiles (of the
+// kernel the shape and accumulator width take) cannot fill the 256 CUs about
+// twice: 512 / tiles splits, at most 16.
+inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int int_bits, int requested) {
   const int ktiles = int(cdiv(K, ktile_for(io_dtype)));
   if (ktiles <= 1) return 1;
   int s;
@@ -1347,8 +1362,9 @@ inline int resolve_splits(int64_t M, int64_t N, int64_t K, int io_dtype, int req
     int bm, bn;
     tile_dims(pick_tile(M), bm, bn);
     if (big_rows(M) && io_dtype != FXPR_DTYPE_F32) {
-      bm = TB2::BM;  // TB64 has the same tile
-      bn = TB2::BN;
+      const bool s64 = ts64_rows(M, int_bits);
+      bm = s64 ? TS64::BM : TB2::BM;  // TB64 has TB2's tile
+      bn = s64 ? TS64::BN : TB2::BN;
     }
     const int64_t tiles = cdiv(M, bm) * cdiv(N, bn);
     if (tiles >= 256) return 1;

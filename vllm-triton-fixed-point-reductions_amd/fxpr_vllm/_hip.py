@@ -41,7 +41,7 @@ SIGNATURES: dict[str, list] = {
     "fxpr_log_softmax_shard_finish": [_P, _I, _P, _P, _P, _I, _L, _L, _I, _P],
     "fxpr_sample_greedy": [_P, _I, _L, _L, _I, _I, _I, _P, _P, _P, _P, _P],
     "fxpr_gemm": [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _P],
-    "fxpr_gemm_splits": [_L, _L, _L, _I, _I],
+    "fxpr_gemm_splits": [_L, _L, _L, _I, _I, _I],
     "fxpr_gemm_partial": [_P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _I, _I, _P],
     "fxpr_gemm_finish": [_P, _P, _P, _I, _L, _L, _L, _L, _I, _I, _P],
     "fxpr_unified_attention": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _I, _I, _L,

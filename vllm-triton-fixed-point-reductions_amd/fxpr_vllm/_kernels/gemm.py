@@ -24,9 +24,10 @@ _BLOCK_K_BY_DTYPE = {
 _SUPPORTED_DTYPES = tuple(_BLOCK_K_BY_DTYPE)
 
 
-def resolve_split_k(M: int, N: int, K: int, dtype: torch.dtype, split_k: int = 0) -> int:
-    """Split count the library will use (0 = its automatic policy)."""
-    return _hip.load().fxpr_gemm_splits(M, N, K, _hip.DTYPE_CODE[dtype], int(split_k))
+def resolve_split_k(M: int, N: int, K: int, dtype: torch.dtype, int_bits: int = 32, split_k: int = 0) -> int:
+    """Split count the library will use for int_bits-bit sums (split_k 0 = its
+    automatic policy)."""
+    return _hip.load().fxpr_gemm_splits(M, N, K, _hip.DTYPE_CODE[dtype], int(int_bits), int(split_k))
 
 
 def gemm_fxp_run(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None, int_bits: int,
