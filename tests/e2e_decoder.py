@@ -93,11 +93,12 @@ class Decoder:
     def _rope(self, x, tables):  # x [T, H, D], rotate-half, fp32 math per element
         # x1 cos - x2 sin | x2 cos + x1 sin: each product rounded, then one
         # add (x2 * -sin is exactly -(x2 * sin)); q and k heads in one call
+        # (x is widened to fp32 inside each product: the same values as
+        # converting it first, one kernel fewer)
         cos, sin = tables
         T, H, D = x.shape
-        xf = x.float()
-        out = xf * cos
-        out += xf.view(T, H, 2, D // 2).flip(2).reshape(T, H, D) * sin
+        out = x * cos
+        out += x.view(T, H, 2, D // 2).flip(2).reshape(T, H, D) * sin
         return out.to(x.dtype)
 
     def step(self, tokens, positions, qsl, seq_lens, block_table, slots, max_q, sample_rows):
@@ -128,6 +129,8 @@ class Decoder:
             h = self._gemm(o.view(T, -1), L["wo"])
             x = torch.ops.fxpr.rms_norm_fxp_residual(h, residual, L["ln2"], c.eps)
             gu = self._gemm(x, L["wgu"])
+            # (both halves widened by one copy: an in-place product with the
+            # bf16 half itself takes a slow path at one row, ~48 us)
             guf = gu.float()
             act = torch.nn.functional.silu(guf[:, :c.ffn])
             act.mul_(guf[:, c.ffn:])
