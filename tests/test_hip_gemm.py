@@ -44,7 +44,7 @@ def _oracle(a, b, bias, bits, frac):
     return from_np(G.gemm(to_np(a), to_np(b), None if bias is None else to_np(bias), io, bits, frac), a.dtype)
 
 
-SHAPES = [(1, 1, 1), (3, 33, 7), (17, 257, 300), (64, 512, 1000), (130, 33, 130), (200, 4096, 256)]
+SHAPES = [(1, 1, 1), (3, 33, 7), (17, 257, 300), (40, 72, 300), (64, 512, 1000), (130, 33, 130), (200, 4096, 256)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

@@ -1229,9 +1229,12 @@ int launch_cfg(GemmArgs a, int splits, hipStream_t st) {
 // e.g. N = 4096 at M = 1: 10 against 17 us; N = 6144: 15 against 18 us;
 // K = 14336: 28 against 34 us. Wider N streams as fast or faster from the
 // long-lived 16 x 256 tiles (N = 28672 / 128256 at M = 1: 43 / 170 us; a
-// persistent form of this kernel took 44 / 185), and M = 32 / 64 from the
-// 128 x 128 tiles split over K (N = 4096: 20 / 23 us; 32- / 64-row fragments
-// here took 16 / 50).
+// persistent form of this kernel took 44 / 185), and M = 17 .. 64 from the
+// large-M kernel's tiles split over K (32-row fragments here: 16-17 against
+// 17-18 us at N = 4096, but 28-31 against 22-23 at N = 6144 and 49-52
+// against 33-34 at K = 14336, with two or four K-tiles in flight, two
+// workgroups per CU or eight waves; 64-row fragments 50 against 23 at
+// N = 4096).
 constexpr int64_t kStreamMaxM = 16, kStreamMaxN = 8192;
 
 // Shapes the decode-shape kernel takes (16-bit inputs, unsplit)
