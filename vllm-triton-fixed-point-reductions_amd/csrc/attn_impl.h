@@ -2258,14 +2258,26 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t n
       wc[k] = wv_p[int64_t(c) * a.head_dim];
     }
   };
+  // Mn is M or mc[k], so fa or fb is 2^0 = 1 (unless both maxima are +inf:
+  // inf - inf is NaN), and rescale(x, 1) = x for 16- and 32-bit sums (exact
+  // in fp64): those rescale one side only. The side is the same for the
+  // whole (token, head), i.e. for every lane of the wave.
   auto fold = [&](int cb, int c_end) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
       if (cb + k >= c_end || mc[k] == -__builtin_inff()) continue;
       float Mn, fa, fb;
       merge_factors(M, mc[k], Mn, fa, fb);
-      D = wadd<BITS>(rescale<BITS>(D, fa), rescale<BITS>(dc[k], fb));
-      W = wadd<BITS>(rescale<BITS>(W, fa), rescale<BITS>(wc[k], fb));
+      if (BITS != 64 && fa == 1.0f) {
+        D = wadd<BITS>(D, rescale<BITS>(dc[k], fb));
+        W = wadd<BITS>(W, rescale<BITS>(wc[k], fb));
+      } else if (BITS != 64 && fb == 1.0f) {
+        D = wadd<BITS>(rescale<BITS>(D, fa), dc[k]);
+        W = wadd<BITS>(rescale<BITS>(W, fa), wc[k]);
+      } else {
+        D = wadd<BITS>(rescale<BITS>(D, fa), rescale<BITS>(dc[k], fb));
+        W = wadd<BITS>(rescale<BITS>(W, fa), rescale<BITS>(wc[k], fb));
+      }
       M = Mn;
     }
   };
