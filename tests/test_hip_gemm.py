@@ -202,6 +202,30 @@ def test_gemm_big_64x256_tiles_exact(dtype, M):
             assert torch.equal(got, want), (bits, s, mismatch_report(got, want))
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_gemm_big_64x256_tiles_random_shapes(seed):
+    # seeded random shapes of the M = 17 .. 64 tiles: M, N, K (K 16-byte
+    # aligned rows, so the large-M kernel takes them; a partial last K-tile
+    # when K is not a multiple of 128), accumulator width, split count and
+    # input type; dyadic inputs (every K-tile dot exact) equal the oracle bit
+    # for bit
+    rng = np.random.default_rng(1000 + seed)
+    for _ in range(6):
+        M = int(rng.integers(17, 65))
+        N = int(rng.integers(1, 700))
+        K = 8 * int(rng.integers(1, 80))
+        bits, frac = [(32, 16), (16, 8), (32, 12)][int(rng.integers(0, 3))]
+        dtype = [torch.bfloat16, torch.float16][int(rng.integers(0, 2))]
+        split = [0, 1, 2, 3, 5][int(rng.integers(0, 5))]
+        g = torch.Generator("cpu").manual_seed(int(rng.integers(0, 1 << 30)))
+        u = (frac + 1) // 2
+        a = _dyadic((M, K), -8, 8, -u, g, dtype)
+        b = _dyadic((K, N), -8, 8, -(frac + 1 - u), g, dtype)
+        got = _run(a, b, bits=bits, frac=frac, b_layout="nk", split_k=split)
+        want = _oracle(a, b, None, bits, frac)
+        assert torch.equal(got, want), (M, N, K, bits, frac, dtype, split, mismatch_report(got, want))
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M", _BIG_M)
 def test_gemm_big_mixed_tile_paths(dtype, M):
