@@ -169,6 +169,11 @@ int fxpr_debug_lsm_fallbacks(unsigned long long* count);
  * k = 0). A log-probability is fl32(x_j) - lse with lse computed exactly as in
  * fxpr_log_softmax(int_bits, frac_bits): the values equal that function's
  * fp32 outputs bit for bit.
+ * workspace (caller-owned, no zeroing) of at least
+ * fxpr_sample_greedy_workspace_bytes(rows, num_logprobs) bytes lets a launch
+ * of few rows (at most 128) spread each row over several workgroups; NULL or
+ * a smaller workspace runs one workgroup per row. The bits are the same
+ * either way.
  * No counterpart exists in the reference: it lists fxpr_vllm/sampling.py
  * (README.md:69) but does not ship it; this is the step after the lm_head
  * GEMM and log_softmax_fxp.
@@ -176,7 +181,11 @@ int fxpr_debug_lsm_fallbacks(unsigned long long* count);
 int fxpr_sample_greedy(const void* logits, int x_dtype, int64_t rows,
                        int64_t cols, int num_logprobs, int int_bits,
                        int frac_bits, int64_t* sampled, float* sampled_logprob,
-                       int64_t* topk_ids, float* topk_logprobs, void* stream);
+                       int64_t* topk_ids, float* topk_logprobs, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+/* Workspace bytes fxpr_sample_greedy can use (0: it runs one workgroup per
+ * row at this row count). */
+int64_t fxpr_sample_greedy_workspace_bytes(int64_t rows, int num_logprobs);
 
 /*
  * Fixed-point GEMM, C[M,N] = IO(fl32(acc) * 2^-frac_bits (+ bias)) with

@@ -97,6 +97,61 @@ def test_top_keys_held_by_few_threads():
         assert ids[3].tolist() == list(range(V - 64, V))
 
 
+def _sample_both_paths(x, k, b, f):
+    """The C entry point without a workspace (one workgroup per row) and with
+    one (rows of at most 128 spread over several workgroups)."""
+    from fxpr_vllm import _hip
+    rows, vocab = x.shape
+    outs = []
+    for use_ws in (False, True):
+        ids = torch.full((rows,), -1, dtype=torch.int64, device=DEV)
+        lp = torch.full((rows,), 7.0, dtype=torch.float32, device=DEV)
+        top = torch.full((rows, k), -1, dtype=torch.int64, device=DEV)
+        top_lp = torch.full((rows, k), 7.0, dtype=torch.float32, device=DEV)
+        ws_bytes = _hip.load().fxpr_sample_greedy_workspace_bytes(rows, k) if use_ws else 0
+        ws = torch.full((max(ws_bytes, 1),), 0xA5, dtype=torch.uint8, device=DEV)  # stale contents
+        _hip.call("fxpr_sample_greedy", x.data_ptr(), _hip.DTYPE_CODE[x.dtype], rows, vocab, k, b, f,
+                  ids.data_ptr(), lp.data_ptr(), top.data_ptr() if k else None, top_lp.data_ptr() if k else None,
+                  ws.data_ptr() if use_ws else None, ws_bytes, _hip.stream_ptr(x.device))
+        outs.append((ids.cpu(), lp.cpu(), top.cpu(), top_lp.cpu()))
+    return outs
+
+
+def _paths_equal(one, multi):
+    # ids exactly; log-probabilities bit for bit, any NaN matching any NaN (a
+    # NaN row's payload may come from different operands on the two paths)
+    assert torch.equal(one[0], multi[0]) and torch.equal(one[2], multi[2])
+    assert _same_bits(one[1].numpy(), multi[1].numpy()) and _same_bits(one[3].numpy(), multi[3].numpy())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,vocab", [(1, 128_256), (32, 128_256), (128, 32_000), (3, 300_001), (5, 8192)])
+@pytest.mark.parametrize("k", [0, 5, 64])
+def test_multi_workgroup_rows_equal_one_workgroup(dtype, rows, vocab, k):
+    # several workgroups per row (span maxima and top keys, span sums against
+    # the row maximum, a per-row merge) give the one-workgroup kernel's bits;
+    # 300001 columns take element loads
+    x = _logits(rows, vocab, seed=rows + vocab + k, dtype=dtype, ties=(k == 64))
+    if rows >= 3:
+        x[0] = 2.0                      # flat: the top 64 all in the first span
+        x[1, vocab // 3] = float("nan")
+        x[2, -5:] = float("inf")
+    one, multi = _sample_both_paths(x.to(DEV), k, 32, 16)
+    _paths_equal(one, multi)
+    if rows == 1 or (rows == 32 and k == 5):  # and the oracle, for a few
+        ids, lp, top, top_lp = S.sample_greedy(to_np(x), IO_NAME[x.dtype], k, 32, 16)
+        assert np.array_equal(multi[0].numpy(), ids) and np.array_equal(multi[2].numpy(), top)
+        assert _same_bits(multi[1].numpy(), lp) and _same_bits(multi[3].numpy(), top_lp)
+
+
+@pytest.mark.parametrize("b,f", [(64, 32), (16, 8), (64, 63)])
+def test_multi_workgroup_formats(b, f):
+    # 64-bit (and 128-bit, Q63) exact sums and 16-bit terms across the spans
+    x = _logits(16, 128_256, seed=b + f, ties=True)
+    one, multi = _sample_both_paths(x.to(DEV), 10, b, f)
+    _paths_equal(one, multi)
+
+
 def test_logprobs_equal_log_softmax_and_tokens_equal_argmax():
     x = _logits(32, 128_256, seed=11).to(DEV)
     ids, lp, top, top_lp = torch.ops.fxpr.sample_greedy_fxp(x, 20, 32, 16)

@@ -170,7 +170,7 @@ extern "C" int fxpr_fixed_to_float(const void* q, int q_dtype, void* y, int floa
   }
 }
 
-extern "C" int fxpr_abi_version(void) { return 2; }
+extern "C" int fxpr_abi_version(void) { return 3; }
 
 extern "C" const char* fxpr_error_string(int code) {
   switch (code) {

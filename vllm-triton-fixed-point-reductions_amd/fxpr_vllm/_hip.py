@@ -39,7 +39,7 @@ SIGNATURES: dict[str, list] = {
     "fxpr_log_softmax_shard_max": [_P, _I, _P, _L, _L, _P],
     "fxpr_log_softmax_shard_sum": [_P, _I, _P, _P, _L, _L, _I, _I, _P],
     "fxpr_log_softmax_shard_finish": [_P, _I, _P, _P, _P, _I, _L, _L, _I, _P],
-    "fxpr_sample_greedy": [_P, _I, _L, _L, _I, _I, _I, _P, _P, _P, _P, _P],
+    "fxpr_sample_greedy": [_P, _I, _L, _L, _I, _I, _I, _P, _P, _P, _P, _P, _L, _P],
     "fxpr_gemm": [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _P],
     "fxpr_gemm_splits": [_L, _L, _L, _I, _I, _I],
     "fxpr_gemm_partial": [_P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _I, _I, _P],
@@ -63,7 +63,11 @@ SIGNATURES: dict[str, list] = {
 RESTYPES = {
     "fxpr_gemm_workspace_bytes": ([_L, _L, _L, _I, _I, _I], _L),
     "fxpr_attention_workspace_bytes": ([_I, _L, _I, _I, _I, _I, _I, _I, _I, _I], _L),
+    "fxpr_sample_greedy_workspace_bytes": ([_L, _I], _L),
 }
+
+# the ABI revision these signatures describe (include/fxpr.h, fxpr_abi_version)
+ABI_VERSION = 3
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()
@@ -87,6 +91,11 @@ def load() -> ctypes.CDLL:
             lib.fxpr_error_string.restype = ctypes.c_char_p
             lib.fxpr_abi_version.argtypes = []
             lib.fxpr_abi_version.restype = _I
+            if lib.fxpr_abi_version() != ABI_VERSION:
+                raise RuntimeError(
+                    f"fxpr: {LIB_PATH} implements ABI revision {lib.fxpr_abi_version()}, these bindings "
+                    f"revision {ABI_VERSION}; rebuild it (`python build.py` in the package directory)"
+                )
             for name, argtypes in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes

@@ -40,8 +40,12 @@ def sample_greedy_fxp_run(logits: torch.Tensor, num_logprobs: int, int_bits: int
     topk_ids = torch.empty(rows, k, device=dev, dtype=torch.int64)
     topk_lp = torch.empty(rows, k, device=dev, dtype=torch.float32)
     if rows:
+        # few rows: the library spreads each row over several workgroups, its
+        # partials in this workspace (caching allocator: capture-safe)
+        ws_bytes = _hip.load().fxpr_sample_greedy_workspace_bytes(rows, k)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes > 0 else None
         _hip.call("fxpr_sample_greedy", x.data_ptr(), _hip.DTYPE_CODE[x.dtype], rows, vocab, k, int(int_bits),
                   int(frac_bits), ids.data_ptr(), lp.data_ptr(), _hip.ptr(topk_ids) if k else None,
-                  _hip.ptr(topk_lp) if k else None, _hip.stream_ptr(dev))
+                  _hip.ptr(topk_lp) if k else None, _hip.ptr(ws), ws_bytes, _hip.stream_ptr(dev))
     lead = tuple(logits.shape[:-1])
     return ids.view(lead), lp.view(lead), topk_ids.view(lead + (k,)), topk_lp.view(lead + (k,))
