@@ -7,8 +7,10 @@
 // fl32(x_j) - lse with lse from row_lse, i.e. exactly the fp32-output
 // log_softmax_fxp value of that element.
 //
-// One workgroup per row, the row held in registers as in the log-softmax.
-// Selection is by rounds: each round takes the largest 64-bit order key
+// One workgroup per row (sample_greedy_kernel), the row held in registers as
+// in the log-softmax; few rows with a workspace instead spread each row over
+// several workgroups (sample_span_kernel, sample_sum_kernel,
+// sample_final_kernel below), with the same bits. Selection is by rounds: each round takes the largest 64-bit order key
 // below the previous round's, key = order(value) << 32 | (0xfffffffe - j),
 // which makes every key of a row distinct, never all ones and never zero.
 // One pass keeps each thread's two largest keys (branchless); a round is
