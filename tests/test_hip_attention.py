@@ -487,3 +487,29 @@ def test_mixed_batch_routes_each_request_and_keeps_bits():
         alone = attend(qi, kv, torch.tensor([0, ql], dtype=torch.int32, device=DEV), sl[i:i + 1].contiguous(),
                        bt[i:i + 1].contiguous(), ql, 0, scale=scale)
         assert torch.equal(both[starts[i]:starts[i] + ql], alone), i
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_strided_query_and_output_views(dtype):
+    # q as the leading columns of a fused q/k/v projection output and o as
+    # columns of a wider buffer (token strides above heads x head_dim, as
+    # vLLM hands them over): the same bits as contiguous tensors on the
+    # decode, short-prompt and prefill-workgroup paths, split and unsplit,
+    # and nothing written outside the view
+    q_lens, ctxs = [1, 300, 1, 5, 1], [2000, 700, 517, 40, 3000]
+    hq, hkv, d = 8, 2, 128
+    q, kv, qsl, sl, bt = _prefix_case(q_lens, ctxs, hq, hkv, d, 16, dtype, seed=33)
+    T = q.shape[0]
+    qkv = torch.full((T, (hq + 2 * hkv) * d), float("nan"), dtype=dtype, device=DEV)
+    qkv[:, :hq * d] = q.reshape(T, hq * d)
+    qv = qkv[:, :hq * d].view(T, hq, d)
+    assert qv.stride() == ((hq + 2 * hkv) * d, d, 1)
+    scale = 1 / math.sqrt(d)
+    for splits in (0, 1):
+        want = attend(q, kv, qsl, sl, bt, max(q_lens), splits, scale=scale)
+        buf = torch.full((T, hq * d + 64), 7.0, dtype=dtype, device=DEV)
+        ov = buf[:, 32:32 + hq * d].view(T, hq, d)
+        torch.ops.fxpr.unified_attention_fxp(qv, kv, ov, qsl, sl, bt, max(q_lens), None, True, scale, 32, 16,
+                                             0.0, 0, splits)
+        assert torch.equal(ov, want), splits
+        assert torch.all(buf[:, :32] == 7.0) and torch.all(buf[:, 32 + hq * d:] == 7.0)

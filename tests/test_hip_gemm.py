@@ -363,6 +363,32 @@ def test_gemm_decode_shape_kernel_matches_split_path(dtype, M):
         assert torch.equal(row[0], _run(a, b, bias, b_layout="nk")[M - 1])
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M", [1, 8, 32, 64, 256])
+def test_gemm_row_strided_a(dtype, M):
+    # A as a view of wider rows (row stride above K, as a column slice of a
+    # fused projection's output is): rows 16-byte aligned (8 elements of
+    # padding: the vector, DMA and decode-shape paths) and not (3: element
+    # loads). Bits equal the contiguous A's and the oracle's on exact dots,
+    # at every M kernel family (decode-shape, 64 x 256, 128 x 128 tiles)
+    g = torch.Generator("cpu").manual_seed(900 + M)
+    K, N = 1024, 640
+    for pad in (8, 3):
+        wide = _dyadic((M, K + pad), -3, 3, -5, g, dtype)
+        b = _dyadic((K, N), -3, 3, 0, g, dtype)
+        bias = _dyadic((N,), -8, 8, -3, g, dtype)
+        ad = wide.to(DEV)[:, :K]
+        assert ad.stride() == (K + pad, 1)
+        bd = b.t().contiguous().to(DEV).t()
+        bias_d = bias.to(DEV)
+        for bits, frac in ((32, 16), (64, 16)):
+            got = KG.gemm_fxp_run(ad, bd, bias_d, bits, frac).cpu()
+            dense = KG.gemm_fxp_run(ad.contiguous(), bd, bias_d, bits, frac).cpu()
+            assert torch.equal(got, dense), (pad, bits, mismatch_report(got, dense))
+            want = _oracle(wide[:, :K].contiguous(), b, bias, bits, frac)
+            assert torch.equal(got, want), (pad, bits, mismatch_report(got, want))
+
+
 # --- restated reference tests (fxpr_vllm/_tests/test_gemm.py) ---------------
 
 @pytest.mark.parametrize("M,N,K", [(4, 4, 16), (3, 7, 16), (1, 1, 32), (8, 16, 32)])
