@@ -513,3 +513,44 @@ def test_strided_query_and_output_views(dtype):
                                              0.0, 0, splits)
         assert torch.equal(ov, want), splits
         assert torch.all(buf[:, :32] == 7.0) and torch.all(buf[:, 32 + hq * d:] == 7.0)
+
+
+def test_long_context_decode_split_invariance_and_reference():
+    # contexts of 131072 and 70001 keys (256 and 137 chunks of 512) beside a
+    # short one: unsplit, auto, 7 and 64 splits and a request of 100 give the
+    # same bits; each row is within the tolerance of a float64 softmax over
+    # all its keys (the reference's one maximum per row), with 131072 keys in
+    # the denominator's 32-bit fixed-point sum
+    hq, hkv, d, ps = 32, 8, 128, 16
+    lens = [131072, 70001, 600]
+    maxb = max(lens) // ps
+    pool = sum(-(-L // ps) for L in lens) + 5
+    g = torch.Generator("cpu").manual_seed(8)
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    bt = torch.zeros(len(lens), maxb, dtype=torch.int32)
+    at = 0
+    for r, L in enumerate(lens):
+        n = -(-L // ps)
+        bt[r, :n] = perm[at:at + n]
+        at += n
+    gd = torch.Generator(DEV).manual_seed(9)
+    kv = torch.randn(pool, 2, ps, hkv, d, generator=gd, device=DEV, dtype=torch.bfloat16)
+    q = (torch.randn(len(lens), hq, d, generator=g) * 2.0).to(torch.bfloat16).to(DEV)
+    qsl = torch.arange(len(lens) + 1, dtype=torch.int32, device=DEV)
+    sl, btd = torch.tensor(lens, dtype=torch.int32, device=DEV), bt.to(DEV)
+    scale = 1 / math.sqrt(d)
+    ref = attend(q, kv, qsl, sl, btd, 1, 1, scale=scale)
+    for s in (0, 7, 64, 100):
+        assert torch.equal(attend(q, kv, qsl, sl, btd, 1, s, scale=scale), ref), s
+    for r, L in enumerate(lens):
+        n = -(-L // ps)
+        pages = kv[bt[r, :n].long().to(DEV)]                     # [n, 2, ps, hkv, d]
+        k = pages[:, 0].reshape(n * ps, hkv, d)[:L].double()
+        v = pages[:, 1].reshape(n * ps, hkv, d)[:L].double()
+        qh = q[r].double().view(hkv, hq // hkv, d)
+        s_ = torch.matmul(qh, k.permute(1, 2, 0).contiguous()) * scale   # [hkv, group, L]
+        p = torch.softmax(s_, dim=-1)
+        want = torch.matmul(p, v.permute(1, 0, 2).contiguous()).reshape(hq, d)
+        err = (ref[r].double() - want).abs()
+        tol = 1e-2 * want.abs() + 1e-2 * want.pow(2).mean().sqrt()
+        assert torch.all(err <= tol), (r, float((err - tol).max()))
