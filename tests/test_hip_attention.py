@@ -554,3 +554,31 @@ def test_long_context_decode_split_invariance_and_reference():
         err = (ref[r].double() - want).abs()
         tol = 1e-2 * want.abs() + 1e-2 * want.pow(2).mean().sqrt()
         assert torch.all(err <= tol), (r, float((err - tol).max()))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_long_prompt_prefill_reference(dtype):
+    # a 4096-token prompt over a 1000-key cached prefix (causal, GQA 4):
+    # unsplit and auto splits give the same bits, and sampled rows (chunk
+    # and row-tile edges, the last row) are within the tolerance of a
+    # float64 softmax over their keys
+    hq, hkv, d, ps, ql, ctx = 32, 8, 128, 16, 4096, 1000
+    q, kv, qsl, sl, bt = _prefix_case([ql], [ctx], hq, hkv, d, ps, dtype, seed=12)
+    scale = 1 / math.sqrt(d)
+    out = attend(q, kv, qsl, sl, bt, ql, 1, scale=scale)
+    assert torch.equal(out, attend(q, kv, qsl, sl, bt, ql, 0, scale=scale))
+    L = ctx + ql
+    n = -(-L // ps)
+    pages = kv[bt[0, :n].long()]
+    k = pages[:, 0].reshape(n * ps, hkv, d)[:L].double().permute(1, 2, 0).contiguous()  # [hkv, d, L]
+    v = pages[:, 1].reshape(n * ps, hkv, d)[:L].double().permute(1, 0, 2).contiguous()  # [hkv, L, d]
+    g = torch.Generator("cpu").manual_seed(13)
+    rows = sorted({0, 1, 63, 64, 511, 512, 2047, ql - 1} | set(torch.randint(0, ql, (16,), generator=g).tolist()))
+    for i in rows:
+        keys = ctx + i + 1
+        qh = q[i].double().view(hkv, hq // hkv, d)
+        p = torch.softmax(torch.matmul(qh, k[:, :, :keys]) * scale, dim=-1)
+        want = torch.matmul(p, v[:, :keys]).reshape(hq, d)
+        err = (out[i].double() - want).abs()
+        tol = 1e-2 * want.abs() + 1e-2 * want.pow(2).mean().sqrt()
+        assert torch.all(err <= tol), (i, float((err - tol).max()))
