@@ -141,6 +141,8 @@ constexpr int kSpanNreg = 8;
 constexpr int kMaxSpans = 16;
 constexpr int kMultiMaxRows = 128;   // from here the one-workgroup kernel fills the CUs
 constexpr int kFinalThreads = 256;   // kMaxSpans * kMaxLogprobs keys, four per thread
+static_assert(kFinalThreads == kSpanThreads, "block_max_key's shared slots are sized for kSpanThreads");
+static_assert(kMaxSpans * kMaxLogprobs % kFinalThreads == 0, "whole keys per thread");
 
 __device__ __forceinline__ float block_maximum(float v, float* smem) {
 #pragma unroll
