@@ -582,3 +582,17 @@ def test_long_prompt_prefill_reference(dtype):
         err = (out[i].double() - want).abs()
         tol = 1e-2 * want.abs() + 1e-2 * want.pow(2).mean().sqrt()
         assert torch.all(err <= tol), (i, float((err - tol).max()))
+
+
+@pytest.mark.parametrize("ps", [16, 32, 64, 128, 256])
+def test_page_sizes_decode_and_prefill(ps):
+    # pages of 16 to 256 keys (the DMA kernels take a wave's 16 key rows from
+    # one page): decode steps and a prompt in one launch, split and unsplit
+    # bits equal, against the oracle
+    q_lens, ctxs = [1, 1, 200, 1], [3000, 777, 300, 64]
+    q, kv, qsl, sl, bt = _prefix_case(q_lens, ctxs, 16, 4, 128, ps, torch.bfloat16, seed=ps)
+    scale = 1 / math.sqrt(128)
+    one = attend(q, kv, qsl, sl, bt, max(q_lens), 1, scale=scale)
+    for s in (0, 3):
+        assert torch.equal(attend(q, kv, qsl, sl, bt, max(q_lens), s, scale=scale), one), s
+    assert close(one, oracle(q, kv, qsl, sl, bt, scale=scale))

@@ -189,3 +189,18 @@ def test_errors():
         torch.ops.fxpr.sample_greedy_fxp(x.double(), 2, 32, 16)
     e = torch.ops.fxpr.sample_greedy_fxp(x[:0], 2, 32, 16)
     assert e[0].shape == (0,) and e[2].shape == (0, 2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("vocab_off", [-8, 0, 8])
+def test_multi_workgroup_threshold(dtype, vocab_off):
+    # rows split into spans only while every span keeps 256 threads' vectors:
+    # at 512 vectors a row takes two spans, one vector less keeps one
+    # workgroup; both sides of the threshold give the one-workgroup bits
+    vec = 16 // torch.tensor([], dtype=dtype).element_size()
+    vocab = 512 * vec + vocab_off
+    x = _logits(6, vocab, seed=vocab, dtype=dtype, ties=True)
+    x[2, -1] = float("inf")
+    for k in (0, 7):
+        one, multi = _sample_both_paths(x.to(DEV), k, 32, 16)
+        _paths_equal(one, multi)
