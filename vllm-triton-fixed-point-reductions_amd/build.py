@@ -45,8 +45,15 @@ COMMON_FLAGS = [
 # is meant to arrive with the loads issued right after it; the optimizer's
 # lane broadcast would wait for it at once, on every workgroup's critical
 # path.
+# gemm_bf16.hip / gemm_f16.hip: the machine scheduler's memory-clause
+# strategy (the kernels' own sched_barrier stages stay as written; inside
+# them it orders the fragment reads and DMAs differently): the large-M GEMM
+# 1-1.5 % faster at M = 256 .. 8192 in crossed A/B runs, same bits.
+_GEMM_SCHED = ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]
 FILE_FLAGS = {
     "rows.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+    "gemm_bf16.hip": _GEMM_SCHED,
+    "gemm_f16.hip": _GEMM_SCHED,
 }
 
 

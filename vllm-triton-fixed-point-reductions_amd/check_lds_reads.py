@@ -52,7 +52,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE))
-from build import COMMON_FLAGS, CSRC, hipcc  # noqa: E402
+from build import COMMON_FLAGS, CSRC, FILE_FLAGS, hipcc  # noqa: E402
 
 DEFAULT_SOURCES = ["gemm_bf16.hip", "gemm_f16.hip", "attn_bf16.hip", "attn_f16.hip"]
 KERNELS = re.compile(r"^(_ZN4fxpr\w*(gemm_big_kernel|attn_dma_kernel|attn_prefill_dma_kernel)\w*):")
@@ -274,7 +274,7 @@ def check_mfma_asm(path: Path) -> dict[str, list[str]]:
 
 def compile_asm(source: Path, out_dir: Path) -> Path:
     out = out_dir / (source.stem + ".s")
-    flags = [f for f in COMMON_FLAGS if f != "-fPIC"]
+    flags = [f for f in COMMON_FLAGS if f != "-fPIC"] + FILE_FLAGS.get(source.name, [])
     res = subprocess.run([hipcc(), *flags, "-S", "--cuda-device-only", str(source), "-o", str(out)],
                          capture_output=True, text=True)
     if res.returncode != 0:
